@@ -1,0 +1,147 @@
+/*
+ * xfold_hip.h -- C ABI of libxfold_hip.so, the MI355X (gfx950) backend for xfold's
+ * Pairformer and diffusion-transformer hot operators.
+ *
+ * Conventions (every entry point):
+ *   - Pointers are device pointers unless stated; the caller owns every buffer, including
+ *     outputs and workspaces (query sizes with the *_workspace_size functions). The
+ *     library never allocates device memory.
+ *   - Work is enqueued asynchronously on `stream` (a hipStream_t passed as void*; NULL is
+ *     the default stream). No entry point synchronises the host.
+ *   - Return value: XFH_OK or an error code; xfh_last_error() then holds a message for the
+ *     calling host thread. Nothing throws across this boundary.
+ *   - Weights follow torch.nn.Linear's layout [out_features, in_features], row-major, in
+ *     the compute dtype. LayerNorm parameters are fp32 (NULL = absent).
+ *   - dtype codes: XFH_F32, XFH_BF16; masks may also be XFH_BOOL (1 byte, nonzero = keep).
+ *
+ * Each declaration names the reference interface it replaces (paths in the reference
+ * repository Zhengye-AIsys/xfold_cpu).
+ */
+#ifndef XFOLD_HIP_H
+#define XFOLD_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define XFH_ABI_VERSION 1
+
+enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
+enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
+
+/* GEMM epilogues of xfh_linear: acc = x @ w^T + bias, a = aux[row % aux_rows, col]. */
+enum {
+  XFH_EPI_STORE = 0,                 /* y  = acc                     */
+  XFH_EPI_MUL_SIGMOID_AUX = 1,       /* y  = acc * sigmoid(a)        */
+  XFH_EPI_SIGMOID_MUL_AUX = 2,       /* y  = sigmoid(acc) * a        */
+  XFH_EPI_ACCUMULATE = 3,            /* y += acc                     */
+  XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE = 4 /* y += acc * sigmoid(a)    */
+};
+
+/* ABI marker; replaces the `packed_weight_api` attribute
+ * (af3_kernels/src/csrc/bindings.cpp:12). */
+int xfh_abi_version(void);
+
+/* Static description of the build (target, HIP version, kernels); replaces
+ * `runtime_info()` (af3_kernels/src/csrc/bindings.cpp:13-20). */
+const char *xfh_runtime_info(void);
+
+/* Message of the last failed call on this host thread ("" if none). Replaces the
+ * TORCH_CHECK -> RuntimeError path of the pybind11 module (af3_kernels/src/csrc/tools.cpp:20-28). */
+const char *xfh_last_error(void);
+
+/* LayerNorm over the last dim of a contiguous [rows, cols] tensor; fp32 statistics.
+ * Replaces the LayerNorm backends of xfold/fastnn/layer_norm.py:55-81 (torch/triton/ipex). */
+int xfh_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols,
+                   const float *weight, const float *bias, float eps,
+                   void *y, int y_dtype, void *stream);
+
+/* Conditioned LayerNorm: y = sigmoid(scale[r % cond_rows]) * LN_noaffine(x[r]) + shift[r % cond_rows].
+ * `scale`/`shift` are [cond_rows, cols] in `aux_dtype` (the two Linear outputs of the
+ * conditioning branch). Replaces AdaptiveLayerNorm.forward's conditioned branch
+ * (xfold/nn/diffusion_transformer.py:57-62) after its two Linears. */
+int xfh_adaptive_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols,
+                            const void *scale, const void *shift, int aux_dtype, int64_t cond_rows,
+                            float eps, void *y, int y_dtype, void *stream);
+
+/* y[m, n] = epilogue(sum_k x[m, k] * w[n, k] + bias[n]); x row stride ldx, y row stride ldy,
+ * aux row stride ldaux (aux in y_dtype). Replaces `linear` (af3_kernels/src/csrc/matrix.cpp,
+ * bound at bindings.cpp:34-36; Python bridge xfold/fastnn/native.py:55-70). */
+int xfh_linear(const void *x, int64_t ldx, const void *w, const float *bias,
+               int64_t m, int64_t k, int64_t n, int dtype,
+               void *y, int64_t ldy, int y_dtype,
+               int epilogue, const void *aux, int64_t ldaux, int64_t aux_rows,
+               void *stream);
+
+/* Rows of the packed GLU weight for f output features (gate and value interleaved in
+ * groups of 16 features, zero rows pad f up to a multiple of 16). */
+int64_t xfh_glu_packed_rows(int64_t f);
+
+/* Packs transition1.weight ([2f, k], first f rows = SiLU gate) into the GLU layout. */
+int xfh_glu_pack_weight(const void *w, int64_t f, int64_t k, int dtype, void *packed, void *stream);
+
+/* y[m, :f] = silu(x @ Wg^T) * (x @ Wv^T) with a packed weight. Replaces `gated_linear_unit`
+ * (af3_kernels/src/csrc/gated_linear_unit.cpp, bindings.cpp:29-32; torch body
+ * xfold/fastnn/gated_linear_unit.py:103-107). */
+int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_t k, int64_t f,
+                          int dtype, void *y, int y_dtype, void *stream);
+
+/* Scaled dot-product attention with additive bias and key mask, flash-style (no [Q, K]
+ * logits in memory). shape = {B, H, Q, K, D, Dv}. strides (elements) =
+ *   {q_b, q_h, q_n,  k_b, k_h, k_n,  v_b, v_h, v_n,  o_b, o_h, o_n,
+ *    mask_b, mask_h, mask_q, mask_k,  bias_b, bias_h, bias_q, bias_k}
+ * (the last dim of q/k/v/out is contiguous; 0 strides broadcast). Semantics of
+ * xfold/fastnn/attention.py:45-66: logits = (q*scale) k^T + bias; masked logits := -1e9;
+ * softmax over keys; @ v. Replaces `dot_product_attention`
+ * (af3_kernels/src/csrc/dot_product_attention.cpp:110-174, bindings.cpp:44-48). */
+int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
+                              const void *mask, int mask_dtype, const void *bias, int bias_dtype,
+                              void *out, const int64_t *shape, const int64_t *strides,
+                              float scale, void *stream);
+
+/* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).
+ * out (contiguous [n, n, c]) receives the update, or the update is added to it when
+ * `accumulate` is nonzero (out may alias pair then). Replaces `triangle_multiplication`
+ * (af3_kernels/src/csrc/triangle_multiplication.cpp:6-73, bindings.cpp:37-43; torch
+ * module xfold/nn/triangle_multiplication.py:71-105). */
+int64_t xfh_triangle_multiplication_workspace_size(int64_t n, int64_t c, int dtype);
+int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *mask, int mask_dtype,
+                                int64_t n, int64_t c, int outgoing,
+                                const float *left_w, const float *left_b, float left_eps,
+                                const void *proj_w, const void *gate_w,
+                                const float *center_w, const float *center_b, float center_eps,
+                                const void *out_w, const void *gating_w, int dtype,
+                                void *out, int out_dtype, int accumulate,
+                                void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Grid (triangle) self-attention over a contiguous [n, n, c] pair tensor: starting node
+ * (transpose = 0) or ending node (transpose = 1). Same output/accumulate contract as
+ * xfh_triangle_multiplication. Replaces GridSelfAttention.forward
+ * (xfold/nn/attention.py:80-105), whose cpp path chains `linear` and
+ * `dot_product_attention` (xfold/nn/attention.py:49-59). */
+int64_t xfh_grid_self_attention_workspace_size(int64_t n, int64_t c, int64_t heads, int dtype);
+int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, int mask_dtype,
+                            int64_t n, int64_t c, int64_t heads, int transpose,
+                            const float *norm_w, const float *norm_b, float eps,
+                            const void *bias_w, const void *q_w, const void *k_w, const void *v_w,
+                            const void *gating_w, const void *out_w, int dtype,
+                            void *out, int out_dtype, int accumulate,
+                            void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Transition: LN -> GLU (packed transition1) -> transition2 over contiguous [rows, c].
+ * Same output/accumulate contract. Replaces Transition.forward (xfold/nn/primitives.py:33-37),
+ * whose GLU goes through `gated_linear_unit` (xfold/fastnn/gated_linear_unit.py:110-122). */
+int64_t xfh_transition_workspace_size(int64_t rows, int64_t c, int64_t f, int dtype);
+int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t f,
+                   const float *norm_w, const float *norm_b, float eps,
+                   const void *w1_packed, const void *w2, int dtype,
+                   void *out, int out_dtype, int accumulate,
+                   void *workspace, int64_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XFOLD_HIP_H */

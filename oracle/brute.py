@@ -1,0 +1,102 @@
+"""Pure-Python loop restatements for tiny shapes (test infrastructure only).
+
+These pin ``oracle.restatement`` without going through ATen's kernels: plain Python
+floats (double precision), explicit index loops written from the mathematics of the
+reference's operators. They are meant for N <= 6 and a handful of channels.
+"""
+
+from __future__ import annotations
+
+import math
+
+
+def layer_norm(rows, weight=None, bias=None, eps=1e-5):
+    """Row LayerNorm: (x - mean) / sqrt(var + eps) * w + b, biased variance
+    (``xfold/fastnn/layer_norm.py:56-59`` = ``F.layer_norm``)."""
+    out = []
+    for row in rows:
+        n = len(row)
+        mean = sum(row) / n
+        var = sum((x - mean) ** 2 for x in row) / n
+        inv = 1.0 / math.sqrt(var + eps)
+        normed = [(x - mean) * inv for x in row]
+        if weight is not None:
+            normed = [y * w for y, w in zip(normed, weight)]
+        if bias is not None:
+            normed = [y + b for y, b in zip(normed, bias)]
+        out.append(normed)
+    return out
+
+
+def _sigmoid(x):
+    return 1.0 / (1.0 + math.exp(-x))
+
+
+def attention(q, k, v, key_valid=None, bias=None):
+    """Single (batch, head) attention with the reference's semantics
+    (``xfold/fastnn/attention.py:45-66``): logits = (q*d^-0.5).k + bias; a key with
+    ``key_valid[j] == False`` gets logit exactly -1e9; softmax over keys; @v.
+
+    q: [Q][D], k: [K][D], v: [K][Dv], bias: [Q][K] or None, key_valid: [K] or None.
+    """
+    d = len(q[0])
+    scale = d ** -0.5
+    out = []
+    for i, qi in enumerate(q):
+        logits = []
+        for j, kj in enumerate(k):
+            s = sum(qi[t] * scale * kj[t] for t in range(d))
+            if bias is not None:
+                s += bias[i][j]
+            if key_valid is not None and not key_valid[j]:
+                s = -1e9
+            logits.append(s)
+        m = max(logits)
+        e = [math.exp(s - m) for s in logits]
+        total = sum(e)
+        p = [x / total for x in e]
+        out.append([sum(p[j] * v[j][c] for j in range(len(k))) for c in range(len(v[0]))])
+    return out
+
+
+def triangle_multiplication(pair, mask, params, outgoing):
+    """Triangle multiplication update for a tiny pair tensor.
+
+    pair: [N][N][C] nested lists; mask: [N][N]; params: dict of nested lists with keys
+    ``left_w, left_b, proj [2C][C], gate [2C][C], center_w, center_b, out [C][C],
+    gating [C][C]`` (nn.Linear layout [out][in]). Follows
+    ``xfold/nn/triangle_multiplication.py:71-105``: a_c = channel 2c, b_c = channel 2c+1 of
+    mask * proj * sigmoid(gate); outgoing out[c,i,j] = sum_k a[c,i,k] b[c,j,k], incoming
+    out[c,i,j] = sum_k a[c,k,j] b[c,k,i]; then LN over c, output projection, gate.
+    """
+    n = len(pair)
+    c = len(pair[0][0])
+
+    def linear(x, w):
+        return [sum(w[o][t] * x[t] for t in range(len(x))) for o in range(len(w))]
+
+    normed = [[layer_norm([pair[i][j]], params["left_w"], params["left_b"])[0] for j in range(n)]
+              for i in range(n)]
+    a = [[[0.0] * n for _ in range(n)] for _ in range(c)]
+    b = [[[0.0] * n for _ in range(n)] for _ in range(c)]
+    for i in range(n):
+        for j in range(n):
+            p = linear(normed[i][j], params["proj"])
+            g = linear(normed[i][j], params["gate"])
+            for ch in range(c):
+                a[ch][i][j] = p[2 * ch] * mask[i][j] * _sigmoid(g[2 * ch])
+                b[ch][i][j] = p[2 * ch + 1] * mask[i][j] * _sigmoid(g[2 * ch + 1])
+    out = [[None] * n for _ in range(n)]
+    for i in range(n):
+        for j in range(n):
+            vec = []
+            for ch in range(c):
+                if outgoing:
+                    vec.append(sum(a[ch][i][t] * b[ch][j][t] for t in range(n)))
+                else:
+                    vec.append(sum(a[ch][t][j] * b[ch][t][i] for t in range(n)))
+            centred = layer_norm([vec], params["center_w"], params["center_b"])[0]
+            projected = linear(centred, params["out"])
+            gate = linear(normed[i][j], params["gating"])
+            out[i][j] = [projected[o] * _sigmoid(gate[o]) for o in range(c)]
+    return out

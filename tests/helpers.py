@@ -1,0 +1,52 @@
+"""Shared test helpers: golden fixtures and the parity metric."""
+
+from __future__ import annotations
+
+import json
+import math
+from pathlib import Path
+
+import numpy as np
+import torch
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+# Parity bars: max |hip - oracle| / RMS(oracle).
+TOL_FP32 = 1e-4
+TOL_BF16 = 2e-2
+
+
+def load_fixture(name: str):
+    data = np.load(GOLDEN / f"{name}.npz", allow_pickle=False)
+    meta = json.loads(str(data["meta"]))
+    inputs, params, outputs = {}, {}, {}
+    for key in data.files:
+        kind, _, rest = key.partition("/")
+        if kind == "in":
+            t = torch.from_numpy(data[key].copy())
+            dt = str(data[f"dtype/{rest}"])
+            inputs[rest] = t.to(torch.bfloat16) if dt == "torch.bfloat16" else t
+        elif kind == "param":
+            params[rest] = torch.from_numpy(data[key].copy())
+        elif kind == "out":
+            outputs[rest] = torch.from_numpy(data[key].copy())
+    return meta, inputs, params, outputs
+
+
+def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    a = actual.detach().to(torch.float64).cpu()
+    e = expected.detach().to(torch.float64).cpu()
+    assert a.shape == e.shape, (a.shape, e.shape)
+    if e.numel() == 0:
+        return 0.0
+    rms = math.sqrt(float((e * e).mean()))
+    err = float((a - e).abs().max())
+    if not math.isfinite(err):
+        return math.inf
+    return err / rms if rms > 0 else err
+
+
+def assert_parity(actual, expected, tol, what=""):
+    err = rel_err(actual, expected)
+    assert err <= tol, f"{what}: max|diff|/rms = {err:.3e} > {tol:.1e}"
+    return err

@@ -1,0 +1,141 @@
+"""CPU-side checks of the drop-in boundary: the C-ABI library loads, exports every symbol
+include/xfold_hip.h declares, and rejects bad arguments before touching a device; the
+Python mirror keeps the reference's names, parameters and guards."""
+
+import ctypes
+import json
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from tests.helpers import load_fixture
+from xfold_cpu_amd.fastnn import config as fastnn_config
+from xfold_cpu_amd.fastnn import native_hip as nh
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "xfold_hip.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"\b(xfh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = nh.load_library()
+    symbols = declared_symbols()
+    assert len(symbols) >= 15
+    for name in symbols:
+        assert hasattr(lib, name), name
+    assert set(symbols) == set(nh.SIGNATURES), "ctypes signature table and header disagree"
+
+
+def test_abi_version_and_runtime_info():
+    lib = nh.load_library()
+    assert lib.xfh_abi_version() == nh.ABI_VERSION
+    info = json.loads(nh.runtime_info())
+    assert info["arch"] == "gfx950" and info["abi"] == nh.ABI_VERSION
+
+
+def test_invalid_arguments_fail_before_any_launch():
+    # Each call below is rejected by argument validation, so no HIP API is reached.
+    with pytest.raises(ValueError, match="dtypes"):
+        nh.call("xfh_layer_norm", None, 7, 4, 4, None, None, 1e-5, None, 0, None)
+    with pytest.raises(ValueError, match="epilogue"):
+        nh.call("xfh_linear", None, 4, None, None, 4, 4, 4, 0, None, 4, 0, 99, None, 4, 0, None)
+    with pytest.raises(ValueError, match="aux"):
+        nh.call("xfh_linear", None, 4, None, None, 4, 4, 4, 0, None, 4, 0, nh.EPI_MUL_SIGMOID_AUX, None, 4, 0, None)
+    with pytest.raises(ValueError, match="head dim"):
+        nh.call("xfh_grid_self_attention", None, 0, None, 2, 8, 512, 4, 0, None, None, 1e-5,
+                None, None, None, None, None, None, 0, None, 0, 0, None, 0, None)
+    shape = (ctypes.c_int64 * 6)(1, 1, 1, 1, 8, 8)
+    strides = (ctypes.c_int64 * 20)()
+    with pytest.raises(ValueError, match="dtype"):
+        nh.call("xfh_dot_product_attention", None, None, None, 5, None, 2, None, 0, None, shape,
+                strides, 1.0, None)
+    lib = nh.load_library()
+    assert "dtype" in lib.xfh_last_error().decode()
+
+
+def test_workspace_too_small_is_reported():
+    lib = nh.load_library()
+    need = lib.xfh_triangle_multiplication_workspace_size(16, 8, nh.BF16)
+    assert need > 0
+    # The pointers are never dereferenced: a 16-byte workspace fails the size check before
+    # any kernel is enqueued (the smallest plan needs far more).
+    fake = ctypes.c_void_p(1 << 40)
+    status = lib.xfh_triangle_multiplication(fake, 1, None, 2, 16, 8, 1, None, None, 1e-5, fake, fake,
+                                             None, None, 1e-5, fake, fake, 1, fake, 1, 0, fake, 16,
+                                             None)
+    assert status == 3 and "workspace" in lib.xfh_last_error().decode()
+    assert lib.xfh_grid_self_attention_workspace_size(8, 32, 4, nh.BF16) > 0
+    assert lib.xfh_transition_workspace_size(64, 128, 512, nh.F32) >= 64 * (128 + 512) * 4
+    assert lib.xfh_glu_packed_rows(5) == 32 and lib.xfh_glu_packed_rows(512) == 1024
+
+
+def test_empty_inputs_are_no_ops():
+    lib = nh.load_library()
+    assert lib.xfh_layer_norm(None, 0, 0, 128, None, None, 1e-5, None, 0, None) == 0
+    assert lib.xfh_linear(None, 4, None, None, 0, 4, 4, 1, None, 4, 1, 0, None, 4, 0, None) == 0
+
+
+def test_config_defaults_to_hip_and_rejects_other_backends():
+    from xfold_cpu_amd import fastnn, nn as hnn
+    for name in ("layer_norm_implementation", "dot_product_attention_implementation",
+                 "gated_linear_unit_implementation", "triangle_multiplication_implementation"):
+        assert getattr(fastnn_config, name) == "hip"
+    saved = fastnn_config.gated_linear_unit_implementation
+    try:
+        fastnn_config.gated_linear_unit_implementation = "torch"
+        with pytest.raises(ValueError, match="only 'hip'"):
+            fastnn.gated_linear_unit(torch.randn(2, 3), torch.randn(3, 4))
+    finally:
+        fastnn_config.gated_linear_unit_implementation = saved
+
+
+def test_guards_reject_cpu_tensors_and_gradients():
+    from xfold_cpu_amd import fastnn
+    with pytest.raises(ValueError, match="ROCm"):
+        fastnn.gated_linear_unit(torch.randn(2, 3), torch.randn(3, 4))
+    with pytest.raises(ValueError, match="ROCm"):
+        fastnn.dot_product_attention(torch.randn(1, 1, 2, 4), torch.randn(1, 1, 2, 4), torch.randn(1, 1, 2, 4))
+    with torch.enable_grad(), pytest.raises(RuntimeError, match="inference only"):
+        nh.check_gpu_inference(torch.randn(2, requires_grad=True, device="meta"))
+
+
+def test_compute_dtype_rules():
+    assert nh.compute_dtype(torch.ones(2), torch.ones(2)) == torch.float32
+    with pytest.raises(ValueError, match="dtypes must match"):
+        nh.compute_dtype(torch.ones(2), torch.ones(2, dtype=torch.bfloat16))
+    with pytest.raises(ValueError):
+        nh.compute_dtype(torch.ones(2, dtype=torch.float16))
+
+
+def test_weight_cache_reuses_and_invalidates():
+    weight = torch.nn.Parameter(torch.randn(7, 5))
+    cache = nh.HipWeightCache()
+    with torch.no_grad():
+        first = cache.get(weight, torch.float32)
+        assert first is cache.get(weight, torch.float32)
+        weight.add_(1)
+        updated = cache.get(weight, torch.float32)
+        assert updated is not first
+        torch.testing.assert_close(updated, weight)
+        assert cache.get(weight, torch.bfloat16).dtype == torch.bfloat16
+    with torch.inference_mode():
+        cache.get(torch.randn(5, 7), torch.float32)
+    assert cache._key is None
+
+
+@pytest.mark.parametrize("fixture,cls", [
+    ("pairformer_block", "PairformerBlock"), ("diffusion_transformer", "DiffusionTransformer"),
+    ("grid_attention_start", "GridSelfAttention"), ("self_attention_cond", "SelfAttention"),
+    ("diffusion_transition", "DiffusionTransition"), ("transition", "Transition")])
+def test_modules_keep_the_reference_parameter_names(fixture, cls):
+    """state_dict keys of the HIP modules equal those of the reference modules (recorded
+    in the golden fixtures), so checkpoints load unchanged."""
+    from xfold_cpu_amd import nn as hnn
+    meta, _, params, _ = load_fixture(fixture)
+    module = getattr(hnn, cls)(**meta["args"])
+    module.load_state_dict(params, strict=True)

@@ -1,0 +1,120 @@
+"""Per-block parity (PairformerBlock, DiffusionTransformer) and the golden fixtures
+through the HIP modules."""
+
+import pytest
+import torch
+
+from oracle import restatement as R
+from tests.helpers import TOL_BF16, TOL_FP32, assert_parity, load_fixture, rel_err
+from tests.test_gpu_ops import announce, autocast, pair_of
+from xfold_cpu_amd import nn as hnn
+from xfold_cpu_amd.synthetic import init_module_, pair_block_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def run_hip_fixture(name, device):
+    meta, inputs, params, outputs = load_fixture(name)
+    module = getattr(hnn, meta["module"])(**meta["args"]).eval()
+    module.load_state_dict(params, strict=True)
+    module.to(device)
+    d = {k: v.to(device) for k, v in inputs.items()}
+    bf16 = meta.get("autocast", False)
+    kind = meta["module"]
+    with torch.inference_mode(), autocast(bf16):
+        if kind == "GridSelfAttention":
+            got = {"out": module(d["pair"], d["mask"])}
+        elif kind == "Transition":
+            got = {"out": module(d["x"])}
+        elif kind == "SelfAttention":
+            got = {"out": module(d["x"], d["mask"], d["pair_logits"], d.get("single_cond"))}
+        elif kind == "DiffusionTransition":
+            got = {"out": module(d["x"], d["single_cond"])}
+        elif kind == "PairformerBlock":
+            pair, single = module(d["pair"].clone(), d["pair_mask"], d["single"].clone(), d["seq_mask"])
+            got = {"pair": pair, "single": single}
+        else:
+            got = {"out": module(d["act"].clone(), d["mask"], d["single_cond"], d["pair_cond"])}
+    return meta, got, outputs
+
+
+@pytest.mark.parametrize("name", ["grid_attention_start", "grid_attention_end", "transition",
+                                  "self_attention", "self_attention_cond", "diffusion_transition",
+                                  "pairformer_block", "diffusion_transformer"])
+def test_golden_vectors_through_hip(device, name):
+    """fp32 golden vectors written by the reference's own modules."""
+    announce("golden", name)
+    meta, got, want = run_hip_fixture(name, device)
+    for key in want:
+        assert_parity(got[key], want[key], TOL_FP32, f"{name}/{key}")
+
+
+def test_golden_bf16_pairformer_block(device):
+    """The reference's CPU bf16-autocast block (LN/softmax in bf16 there, fp32 here)."""
+    meta, got, want = run_hip_fixture("pairformer_block_bf16", device)
+    for key in want:
+        assert_parity(got[key], want[key], 5e-2, f"bf16 block/{key}")
+
+
+def block_case(n, c_single, bf16, pad, seed, device, with_single=True):
+    args = dict(n_heads=16, c_pair=128, c_single=c_single, n_heads_pair=4, with_single=with_single)
+    ref, hip = pair_of("PairformerBlock", args, seed=seed, device=device)
+    inp = pair_block_inputs(n, c_single=c_single, pad=pad, seed=seed, with_single=with_single)
+    pair, single = inp.pair, inp.single
+    if bf16:
+        pair = pair.bfloat16()
+        single = single.bfloat16() if single is not None else None
+    with torch.inference_mode():
+        if with_single:
+            want_pair, want_single = ref(pair.float().clone(), inp.pair_mask, single.float().clone(), inp.seq_mask)
+        else:
+            want_pair, want_single = ref(pair.float().clone(), inp.pair_mask), None
+        dp = pair.to(device).contiguous()
+        ds = single.to(device).contiguous() if single is not None else None
+        with autocast(bf16):
+            if with_single:
+                got_pair, got_single = hip(dp, inp.pair_mask.to(device), ds, inp.seq_mask.to(device))
+            else:
+                got_pair, got_single = hip(dp, inp.pair_mask.to(device)), None
+    return (got_pair, want_pair), (got_single, want_single)
+
+
+@pytest.mark.parametrize("n,bf16", [(24, False), (48, True), (96, True)])
+def test_pairformer_block(device, n, bf16):
+    announce("pairformer_block", n, bf16)
+    (gp, wp), (gs, ws) = block_case(n, 384, bf16, pad=3, seed=n, device=device)
+    tol = TOL_BF16 if bf16 else TOL_FP32
+    assert gp.dtype == (torch.bfloat16 if bf16 else torch.float32)
+    assert_parity(gp, wp, tol, "pair")
+    assert_parity(gs, ws, tol, "single")
+
+
+def test_pairformer_block_updates_in_place(device):
+    args = dict(n_heads=4, c_pair=128, c_single=64, n_heads_pair=4)
+    _, hip = pair_of("PairformerBlock", args, seed=1, device=device)
+    inp = pair_block_inputs(16, c_single=64, seed=1)
+    pair, single = inp.pair.to(device), inp.single.to(device)
+    with torch.inference_mode():
+        p2, s2 = hip(pair, inp.pair_mask.to(device), single, inp.seq_mask.to(device))
+    assert p2.data_ptr() == pair.data_ptr() and s2.data_ptr() == single.data_ptr()
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_diffusion_transformer_batched_samples(device, bf16):
+    """Five samples batched in one call equal the reference's one-sample-at-a-time loop."""
+    announce("diffusion_transformer", bf16)
+    args = dict(c_act=256, c_single_cond=64, c_pair_cond=32, num_head=16, num_blocks=4, super_block_size=2)
+    ref, hip = pair_of("DiffusionTransformer", args, seed=11, device=device)
+    torch.manual_seed(11)
+    n, samples = 33, 5
+    act = torch.randn(samples, n, 256)
+    mask = torch.ones(n)
+    mask[-2:] = 0
+    scond, pcond = torch.randn(n, 64), torch.randn(n, n, 32)
+    if bf16:
+        act = act.bfloat16()
+    with torch.inference_mode():
+        want = torch.stack([ref(act[s].float().clone(), mask, scond, pcond) for s in range(samples)])
+        with autocast(bf16):
+            got = hip(act.to(device).clone(), mask.to(device), scond.to(device), pcond.to(device))
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "diffusion transformer")

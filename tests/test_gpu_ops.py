@@ -1,0 +1,269 @@
+"""Per-operator parity of the HIP backend against the CPU oracle (oracle/restatement.py).
+
+Bars (max |hip - oracle| / RMS(oracle)): fp32 mode 1e-4, bf16 mode 2e-2. In bf16 mode the
+oracle runs in fp32 on the same bf16-rounded inputs and fp32 weights (the exact answer for
+those inputs); the HIP path computes under CUDA bf16 autocast like the reference's GPU run.
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import restatement as R
+from tests.helpers import TOL_BF16, TOL_FP32, assert_parity, rel_err
+from xfold_cpu_amd import fastnn
+from xfold_cpu_amd import nn as hnn
+from xfold_cpu_amd.fastnn import native_hip as nh
+from xfold_cpu_amd.fastnn import ops
+from xfold_cpu_amd.synthetic import init_module_
+
+pytestmark = pytest.mark.gpu
+
+
+def announce(*what):
+    print("[case]", *what, flush=True)
+
+
+def pair_of(cls_name, args, seed=0, device="cuda"):
+    """(oracle module on CPU fp32, HIP module on device) with identical jittered weights."""
+    ref = init_module_(getattr(R, cls_name)(**args).eval(), seed=seed, ln_jitter=True)
+    hip = getattr(hnn, cls_name)(**args).eval()
+    hip.load_state_dict(ref.state_dict())
+    return ref, hip.to(device)
+
+
+def autocast(enabled):
+    return torch.amp.autocast("cuda", dtype=torch.bfloat16, enabled=enabled)
+
+
+# ---------------------------------------------------------------------------- LayerNorm
+
+@pytest.mark.parametrize("cols", [128, 384, 768, 7, 100])
+@pytest.mark.parametrize("dt_in,dt_out", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("affine", ["full", "weight", "none"])
+def test_layer_norm(device, cols, dt_in, dt_out, affine):
+    announce("layer_norm", cols, dt_in, dt_out, affine)
+    torch.manual_seed(cols)
+    x = (torch.randn(301, cols) * 3 + 1).to(dt_in)
+    w = torch.randn(cols) if affine != "none" else None
+    b = torch.randn(cols) if affine == "full" else None
+    want = F.layer_norm(x.float(), (cols,), w, b, 1e-5)
+    got = ops.layer_norm(x.to(device), (cols,), None if w is None else w.to(device),
+                         None if b is None else b.to(device), 1e-5, out_dtype=dt_out)
+    assert got.dtype == dt_out
+    tol = TOL_FP32 if dt_out == torch.float32 and dt_in == torch.float32 else TOL_BF16
+    assert_parity(got, want, tol, "layer_norm")
+
+
+def test_layer_norm_module_dtype_contract(device):
+    ln = fastnn.LayerNorm(128).eval().to(device)
+    x = torch.randn(4, 128, device=device, dtype=torch.bfloat16)
+    with torch.inference_mode():
+        assert ln(x).dtype == torch.bfloat16
+        with autocast(True):
+            assert ln(x).dtype == torch.float32        # CUDA autocast runs layer_norm in fp32
+        assert ln(x.float()).dtype == torch.float32
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_adaptive_layer_norm(device, dtype):
+    announce("adaptive_layer_norm", dtype)
+    torch.manual_seed(1)
+    x = torch.randn(3, 40, 768).to(dtype)
+    scale, shift = torch.randn(40, 768).to(dtype), torch.randn(40, 768).to(dtype)
+    want = torch.sigmoid(scale.float()) * F.layer_norm(x.float(), (768,)) + shift.float()
+    got = ops.adaptive_layer_norm(x.to(device), scale.to(device), shift.to(device), 1e-5, dtype)
+    assert_parity(got, want, TOL_FP32 if dtype == torch.float32 else TOL_BF16, "adaptive_ln")
+
+
+# ---------------------------------------------------------------------------- Linear / GLU
+
+@pytest.mark.parametrize("m,k,n", [(1, 7, 5), (77, 128, 128), (300, 384, 200), (129, 96, 257)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("epi", [nh.EPI_STORE, nh.EPI_MUL_SIGMOID_AUX, nh.EPI_SIGMOID_MUL_AUX,
+                                 nh.EPI_ACCUMULATE, nh.EPI_MUL_SIGMOID_AUX_ACCUMULATE])
+def test_linear_epilogues(device, m, k, n, dtype, epi):
+    announce("linear", m, k, n, dtype, epi)
+    torch.manual_seed(m + k + n)
+    x = torch.randn(m, k).to(dtype)
+    w = (torch.randn(n, k) / math.sqrt(k)).to(dtype)
+    bias = torch.randn(n)
+    aux = torch.randn(m, n).to(dtype)
+    c0 = torch.randn(m, n).to(dtype)
+    acc = x.float() @ w.float().T + bias
+    want = {nh.EPI_STORE: acc, nh.EPI_MUL_SIGMOID_AUX: acc * torch.sigmoid(aux.float()),
+            nh.EPI_SIGMOID_MUL_AUX: torch.sigmoid(acc) * aux.float(),
+            nh.EPI_ACCUMULATE: c0.float() + acc,
+            nh.EPI_MUL_SIGMOID_AUX_ACCUMULATE: c0.float() + acc * torch.sigmoid(aux.float())}[epi]
+    out = c0.to(device).clone()
+    needs_aux = epi in (nh.EPI_MUL_SIGMOID_AUX, nh.EPI_SIGMOID_MUL_AUX, nh.EPI_MUL_SIGMOID_AUX_ACCUMULATE)
+    ops.linear(x.to(device), w.to(device), bias.to(device), dtype, out=out, epilogue=epi,
+               aux=aux.to(device) if needs_aux else None)
+    assert_parity(out, want, TOL_FP32 if dtype == torch.float32 else TOL_BF16, "linear")
+
+
+def test_linear_aux_rows_broadcast(device):
+    torch.manual_seed(2)
+    x, w, aux = torch.randn(3, 10, 64), torch.randn(32, 64) / 8, torch.randn(10, 32)
+    want = (x @ w.T) * torch.sigmoid(aux)
+    got = ops.linear(x.to(device), w.to(device), None, torch.float32, epilogue=nh.EPI_MUL_SIGMOID_AUX,
+                     aux=aux.to(device), aux_rows=10)
+    assert_parity(got, want, TOL_FP32, "aux rows")
+
+
+@pytest.mark.parametrize("m,k,f", [(6, 7, 5), (1000, 128, 512), (333, 384, 1536), (50, 768, 1536)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_linear_unit(device, m, k, f, dtype):
+    announce("glu", m, k, f, dtype)
+    torch.manual_seed(k)
+    x = torch.randn(m, k).to(dtype)
+    weight = (torch.randn(2 * f, k) / math.sqrt(k)).T.to(dtype)      # [K, 2F] like transition1.weight.T
+    want = R.gated_linear_unit(x.float(), weight.float())
+    got = fastnn.gated_linear_unit(x.to(device), weight.to(device))
+    assert_parity(got, want, TOL_FP32 if dtype == torch.float32 else TOL_BF16, "glu")
+
+
+# ---------------------------------------------------------------------------- attention
+
+@pytest.mark.parametrize("mask_rank", [1, 2, 4])
+@pytest.mark.parametrize("batched", [True, False])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_reference_cases(device, mask_rank, batched, dtype):
+    """The reference's own attention case (tests/test_cpu_runtime.py:70-89): odd head dim 7."""
+    torch.manual_seed(42)
+    q, k, v = [torch.randn(*s).to(dtype) for s in ((1, 2, 3, 7), (1, 2, 5, 7), (1, 2, 5, 4))]
+    mask = torch.tensor([1, 1, 0, 1, 0], dtype=torch.bool)
+    expanded = mask[None, None, None, :]
+    passed = mask if mask_rank == 1 else mask[None] if mask_rank == 2 else expanded
+    bias = torch.randn(1, 2, 3, 5).to(dtype)
+    want = R.dot_product_attention(q.float(), k.float(), v.float(), passed, bias.float())
+    if not batched:
+        q, k, v, bias, want = q[0], k[0], v[0], bias[0], want[0]
+    got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device), passed.to(device),
+                                       bias.to(device))
+    assert_parity(got, want, TOL_FP32 if dtype == torch.float32 else TOL_BF16, "attention")
+
+
+@pytest.mark.parametrize("shape", [(3, 4, 37, 37, 32), (1, 16, 100, 100, 24), (2, 16, 70, 70, 48),
+                                   (2, 3, 65, 130, 64), (1, 1, 1, 1, 16)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_shapes_masks_and_fully_masked_rows(device, shape, dtype):
+    B, H, Q, K, D = shape
+    announce("attention", shape, dtype)
+    torch.manual_seed(Q + K)
+    q, k, v = torch.randn(B, H, Q, D).to(dtype), torch.randn(B, H, K, D).to(dtype), torch.randn(B, H, K, D).to(dtype)
+    bias = torch.randn(H, Q, K).to(dtype)
+    mask = torch.rand(B, K) > 0.25
+    mask[0] = False                      # a fully masked batch row: uniform average of v
+    want = R.dot_product_attention(q.float(), k.float(), v.float(), mask, bias.float())
+    got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device), mask.to(device),
+                                       bias.to(device))
+    assert_parity(got, want, TOL_FP32 if dtype == torch.float32 else TOL_BF16, "attention")
+    assert_parity(got[0], v[0].float().mean(1, keepdim=True).expand(H, Q, D),
+                  TOL_FP32 if dtype == torch.float32 else TOL_BF16, "uniform row")
+
+
+def test_attention_float_mask_and_no_bias(device):
+    torch.manual_seed(3)
+    q, k, v = torch.randn(2, 2, 9, 16), torch.randn(2, 2, 11, 16), torch.randn(2, 2, 11, 16)
+    mask = (torch.rand(2, 11) > 0.5).float()
+    want = R.dot_product_attention(q, k, v, mask, None)
+    got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device), mask.to(device), None)
+    assert_parity(got, want, TOL_FP32, "float mask")
+    want = F.scaled_dot_product_attention(q, k, v)
+    got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device))
+    assert_parity(got, want, TOL_FP32, "sdpa")
+
+
+# ---------------------------------------------------------------------------- modules
+
+def run_both(ref, hip, ref_inputs, dev_inputs, bf16, call=None):
+    call = call or (lambda m, *a: m(*a))
+    with torch.inference_mode():
+        want = call(ref, *ref_inputs)
+        with autocast(bf16):
+            got = call(hip, *dev_inputs)
+    return got, want
+
+
+@pytest.mark.parametrize("n", [5, 37, 64])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_triangle_multiplication(device, n, outgoing, bf16):
+    announce("trimul", n, outgoing, bf16)
+    ref, hip = pair_of("TriangleMultiplication", dict(c_pair=128, _outgoing=outgoing), seed=n)
+    torch.manual_seed(n)
+    pair = torch.randn(n, n, 128)
+    seq = torch.ones(n)
+    seq[-2:] = 0
+    mask = seq[:, None] * seq[None, :]
+    if bf16:
+        pair = pair.bfloat16()
+    got, want = run_both(ref, hip, (pair.float(), mask), (pair.to(device), mask.to(device)), bf16)
+    assert got.dtype == (torch.bfloat16 if bf16 else torch.float32)
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "trimul")
+
+
+@pytest.mark.parametrize("n", [5, 37, 70])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_grid_self_attention(device, n, transpose, bf16):
+    announce("grid_attention", n, transpose, bf16)
+    ref, hip = pair_of("GridSelfAttention", dict(c_pair=128, num_head=4, transpose=transpose), seed=n)
+    torch.manual_seed(n + 1)
+    pair = torch.randn(n, n, 128)
+    seq = torch.ones(n)
+    seq[-3:] = 0
+    mask = seq[:, None] * seq[None, :]
+    mask[1, 2] = 0                       # asymmetric: the ending node must not transpose it
+    if bf16:
+        pair = pair.bfloat16()
+    got, want = run_both(ref, hip, (pair.float(), mask), (pair.to(device), mask.to(device)), bf16)
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "grid attention")
+
+
+@pytest.mark.parametrize("c,f,rows", [(128, 4, (33, 17)), (384, 4, (50,)), (16, 4, (2, 5))])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_transition(device, c, f, rows, bf16):
+    announce("transition", c, f, rows, bf16)
+    ref, hip = pair_of("Transition", dict(c_x=c, num_intermediate_factor=f), seed=c)
+    x = torch.randn(*rows, c)
+    if bf16:
+        x = x.bfloat16()
+    got, want = run_both(ref, hip, (x.float(),), (x.to(device),), bf16)
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "transition")
+
+
+@pytest.mark.parametrize("cond", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_self_attention(device, cond, bf16):
+    c, heads, n = (768, 16, 40) if cond else (384, 16, 50)
+    announce("self_attention", cond, bf16)
+    ref, hip = pair_of("SelfAttention", dict(c_x=c, c_single_cond=384, num_head=heads, use_single_cond=cond),
+                       seed=7)
+    torch.manual_seed(8)
+    x = torch.randn(2, n, c) if cond else torch.randn(n, c)
+    mask = torch.ones(n)
+    mask[-4:] = 0
+    logits = torch.randn(heads, n, n)
+    single = torch.randn(n, 384) if cond else None
+    if bf16:
+        x = x.bfloat16()
+        logits = logits.bfloat16()
+    dev = [t.to(device) if t is not None else None for t in (x, mask, logits, single)]
+    got, want = run_both(ref, hip, (x.float(), mask, logits.float(), single), dev, bf16)
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "self attention")
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_diffusion_transition(device, bf16):
+    announce("diffusion_transition", bf16)
+    ref, hip = pair_of("DiffusionTransition", dict(c_x=768, c_single_cond=384, use_single_cond=True), seed=9)
+    x, cond = torch.randn(2, 30, 768), torch.randn(30, 384)
+    if bf16:
+        x = x.bfloat16()
+    got, want = run_both(ref, hip, (x.float(), cond), (x.to(device), cond.to(device)), bf16)
+    assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "diffusion transition")

@@ -1,0 +1,228 @@
+"""Pins the CPU oracle (oracle/restatement.py) before it is trusted as the checker.
+
+Closed forms restated from the reference's own tests (tests/test_cpu_runtime.py:52-115 in
+the reference), brute-force loops at tiny sizes, invariants of the mathematics, and the
+golden fixtures written from the reference's modules (tests/golden/make_golden.py).
+"""
+
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import brute
+from oracle import restatement as R
+from tests.helpers import load_fixture, rel_err
+
+torch.manual_seed(42)
+
+
+# ------------------------------------------------------------------ closed forms
+
+@pytest.mark.parametrize("affine,bias", [(True, True), (True, False), (False, False)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_layer_norm_matches_functional(affine, bias, dtype):
+    layer = R.LayerNorm(7, elementwise_affine=affine, bias=bias)
+    if affine:
+        with torch.no_grad():
+            layer.weight.normal_()
+            if bias:
+                layer.bias.normal_()
+    x = torch.randn(2, 7, 3).transpose(1, 2).to(dtype)
+    expected = F.layer_norm(x, (7,), layer.weight, layer.bias, layer.eps)
+    torch.testing.assert_close(layer(x), expected, rtol=0, atol=0)
+
+
+def test_layer_norm_matches_brute_force():
+    x = torch.randn(5, 9, dtype=torch.float64)
+    w, b = torch.randn(9, dtype=torch.float64), torch.randn(9, dtype=torch.float64)
+    got = F.layer_norm(x, (9,), w, b, 1e-5)
+    want = torch.tensor(brute.layer_norm(x.tolist(), w.tolist(), b.tolist()), dtype=torch.float64)
+    assert rel_err(got, want) < 1e-12
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_glu_first_half_is_the_silu_gate(dtype):
+    x = torch.randn(2, 3, 7).to(dtype)
+    weight = torch.randn(10, 7).T.to(dtype)
+    a, b = (x @ weight).chunk(2, dim=-1)
+    torch.testing.assert_close(R.gated_linear_unit(x, weight), F.silu(a) * b)
+    # Swapping the halves must change the result (the gate is not symmetric).
+    assert not torch.allclose(R.gated_linear_unit(x, weight), F.silu(b) * a)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("batched", [True, False])
+@pytest.mark.parametrize("mask_rank", [1, 2, 4])
+def test_attention_matches_einsum_restatement(dtype, batched, mask_rank):
+    q, k, v = [torch.randn(*s).to(dtype) for s in ((1, 2, 3, 7), (1, 2, 5, 7), (1, 2, 5, 4))]
+    mask = torch.tensor([1, 1, 0, 1, 0], dtype=torch.bool)
+    expanded = mask[None, None, None, :]
+    passed = mask if mask_rank == 1 else mask[None] if mask_rank == 2 else expanded
+    bias = torch.randn(1, 2, 3, 5).to(dtype)
+    logits = torch.einsum("bhqd,bhkd->bhqk", q * 7 ** -0.5, k) + bias
+    logits.masked_fill_(~expanded, -1e9)
+    expected = torch.einsum("bhqk,bhkd->bhqd", logits.softmax(-1), v)
+    if not batched:
+        q, k, v, bias, expected = q[0], k[0], v[0], bias[0], expected[0]
+    got = R.dot_product_attention(q, k, v, passed, bias)
+    tol = 0.02 if dtype == torch.bfloat16 else 1e-5
+    torch.testing.assert_close(got, expected, rtol=tol, atol=tol if dtype == torch.bfloat16 else 1e-6)
+
+
+def test_attention_matches_brute_force_and_fully_masked_row_is_uniform():
+    q, k, v = torch.randn(4, 6, dtype=torch.float64), torch.randn(5, 6, dtype=torch.float64), \
+        torch.randn(5, 3, dtype=torch.float64)
+    bias = torch.randn(4, 5, dtype=torch.float64)
+    valid = [True, False, True, True, False]
+    got = R.dot_product_attention(q[None, None], k[None, None], v[None, None],
+                                  torch.tensor(valid), bias[None, None])[0, 0]
+    want = torch.tensor(brute.attention(q.tolist(), k.tolist(), v.tolist(), valid, bias.tolist()),
+                        dtype=torch.float64)
+    assert rel_err(got, want) < 1e-12
+    # A row whose keys are all masked averages v uniformly over all keys (-1e9 is finite).
+    none = torch.zeros(5, dtype=torch.bool)
+    got = R.dot_product_attention(q[None, None], k[None, None], v[None, None], none, bias[None, None])[0, 0]
+    assert rel_err(got, v.mean(0).expand(4, 3)) < 1e-12
+
+
+def test_attention_without_bias_or_mask_is_sdpa():
+    q, k, v = torch.randn(2, 3, 5, 8), torch.randn(2, 3, 7, 8), torch.randn(2, 3, 7, 8)
+    got = R.dot_product_attention(q, k, v)
+    torch.testing.assert_close(got, F.scaled_dot_product_attention(q, k, v), rtol=1e-5, atol=1e-6)
+
+
+def test_chunked_attention_equals_unchunked():
+    q, k, v = torch.randn(9, 2, 6, 4), torch.randn(9, 2, 6, 4), torch.randn(9, 2, 6, 4)
+    mask = torch.rand(9, 6) > 0.3
+    bias = torch.randn(2, 6, 6)
+    full = R.dot_product_attention(q, k, v, mask, bias)
+    torch.testing.assert_close(R.dot_product_attention_chunked(q, k, v, mask, bias, rows_per_chunk=4), full)
+
+
+@pytest.mark.parametrize("outgoing", [False, True])
+def test_triangle_directions_match_explicit_channel_contractions(outgoing):
+    layer = R.TriangleMultiplication(8, _outgoing=outgoing).eval()
+    pair, mask = torch.randn(3, 3, 8), torch.eye(3)
+    with torch.no_grad():
+        normalized = layer.left_norm_input(pair)
+        projected = layer.projection(normalized) * mask[..., None] * layer.gate(normalized).sigmoid()
+        a, b = projected[..., 0::2], projected[..., 1::2]
+        product = torch.stack([a[..., c] @ b[..., c].T if outgoing else b[..., c].T @ a[..., c]
+                               for c in range(8)], dim=-1)
+        expected = layer.output_projection(layer.center_norm(product)) * \
+            layer.gating_linear(normalized).sigmoid()
+        torch.testing.assert_close(layer(pair, mask), expected)
+
+
+@pytest.mark.parametrize("outgoing", [False, True])
+def test_triangle_matches_brute_force(outgoing):
+    torch.manual_seed(3)
+    n, c = 4, 6
+    layer = R.TriangleMultiplication(c, _outgoing=outgoing).double().eval()
+    with torch.no_grad():
+        for p in layer.parameters():
+            p.normal_(0, 0.5)
+    pair = torch.randn(n, n, c, dtype=torch.float64)
+    mask = (torch.rand(n, n) > 0.2).double()
+    params = {"left_w": layer.left_norm_input.weight.tolist(), "left_b": layer.left_norm_input.bias.tolist(),
+              "proj": layer.projection.weight.tolist(), "gate": layer.gate.weight.tolist(),
+              "center_w": layer.center_norm.weight.tolist(), "center_b": layer.center_norm.bias.tolist(),
+              "out": layer.output_projection.weight.tolist(), "gating": layer.gating_linear.weight.tolist()}
+    want = torch.tensor(brute.triangle_multiplication(pair.tolist(), mask.tolist(), params, outgoing),
+                        dtype=torch.float64)
+    with torch.no_grad():
+        got = layer(pair, mask)
+    assert rel_err(got, want) < 1e-10
+
+
+def test_triangle_all_ones_mask_equals_no_mask():
+    layer = R.TriangleMultiplication(8).eval()
+    pair = torch.randn(5, 5, 8)
+    with torch.no_grad():
+        torch.testing.assert_close(layer(pair, torch.ones(5, 5)), layer(pair, None))
+
+
+def test_outgoing_of_transpose_is_incoming():
+    """incoming(z)[i,j] = sum_k a[k,j] b[k,i] = outgoing(z^T)[j,i] with the same weights
+    (and the transposed mask); a mistake in either equation's indices breaks it."""
+    torch.manual_seed(5)
+    out_layer = R.TriangleMultiplication(8, _outgoing=True).eval()
+    in_layer = R.TriangleMultiplication(8, _outgoing=False).eval()
+    with torch.no_grad():
+        for p in out_layer.parameters():
+            p.normal_(0, 0.5)
+    in_layer.load_state_dict(out_layer.state_dict())
+    pair = torch.randn(5, 5, 8)
+    mask = (torch.rand(5, 5) > 0.3).float()
+    with torch.no_grad():
+        lhs = out_layer(pair.transpose(0, 1).contiguous(), mask.T.contiguous()).transpose(0, 1)
+        rhs = in_layer(pair, mask)
+    torch.testing.assert_close(lhs, rhs, rtol=1e-5, atol=1e-5)
+    assert rel_err(out_layer(pair, mask), rhs) > 1e-2      # the directions do differ
+
+
+# ------------------------------------------------------------------ golden fixtures
+
+MODULES = {
+    "GridSelfAttention": R.GridSelfAttention,
+    "Transition": R.Transition,
+    "SelfAttention": R.SelfAttention,
+    "DiffusionTransition": R.DiffusionTransition,
+    "PairformerBlock": R.PairformerBlock,
+    "DiffusionTransformer": R.DiffusionTransformer,
+}
+
+
+def run_oracle_on_fixture(name):
+    meta, inputs, params, outputs = load_fixture(name)
+    module = MODULES[meta["module"]](**meta["args"]).eval()
+    module.load_state_dict(params, strict=True)            # pins parameter names and shapes
+    autocast = meta.get("autocast", False)
+    with torch.inference_mode(), torch.amp.autocast("cpu", dtype=torch.bfloat16, enabled=autocast):
+        kind = meta["module"]
+        if kind == "GridSelfAttention":
+            got = {"out": module(inputs["pair"], inputs["mask"])}
+        elif kind == "Transition":
+            got = {"out": module(inputs["x"])}
+        elif kind == "SelfAttention":
+            got = {"out": module(inputs["x"], inputs["mask"], inputs["pair_logits"], inputs.get("single_cond"))}
+        elif kind == "DiffusionTransition":
+            got = {"out": module(inputs["x"], inputs["single_cond"])}
+        elif kind == "PairformerBlock":
+            pair, single = module(inputs["pair"].clone(), inputs["pair_mask"], inputs["single"].clone(),
+                                  inputs["seq_mask"])
+            got = {"pair": pair, "single": single}
+        else:
+            got = {"out": module(inputs["act"].clone(), inputs["mask"], inputs["single_cond"],
+                                 inputs["pair_cond"])}
+    return meta, got, outputs
+
+
+@pytest.mark.parametrize("name", ["grid_attention_start", "grid_attention_end", "transition",
+                                  "self_attention", "self_attention_cond", "diffusion_transition",
+                                  "pairformer_block", "pairformer_block_bf16", "diffusion_transformer"])
+def test_oracle_reproduces_reference_golden_vectors(name):
+    meta, got, want = run_oracle_on_fixture(name)
+    tol = 1e-6 if not meta.get("autocast") else 1e-2
+    for key in want:
+        err = rel_err(got[key], want[key])
+        assert err <= tol, f"{name}/{key}: {err:.3e}"
+
+
+def test_golden_catches_a_transposed_bias():
+    """A plausible restatement mistake (bias taken from the transposed pair in the ending
+    node) must fail the golden check."""
+    meta, inputs, params, outputs = load_fixture("grid_attention_end")
+    module = R.GridSelfAttention(**meta["args"]).eval()
+    module.load_state_dict(params)
+    with torch.inference_mode():
+        normed = module.act_norm(inputs["pair"])
+        wrong_bias = module.pair_bias_projection(normed.permute(1, 0, 2)).permute(2, 0, 1)
+        x = normed.permute(1, 0, 2)
+        q, k, v = (R._heads_first(getattr(module, n)(x), module.num_head)
+                   for n in ("q_projection", "k_projection", "v_projection"))
+        o = R._heads_last(R.dot_product_attention(q, k, v, inputs["mask"], wrong_bias))
+        o = module.output_projection(o * torch.sigmoid(module.gating_query(x))).permute(1, 0, 2)
+    assert rel_err(o, outputs["out"]) > 1e-3

@@ -1,0 +1,346 @@
+// C ABI of libxfold_hip.so: validation, workspace carving and kernel sequencing.
+// Declarations and their reference counterparts are in include/xfold_hip.h.
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace xfh {
+
+static thread_local std::string g_last_error;
+
+void set_error(const std::string &message) { g_last_error = message; }
+
+int fail(int code, const std::string &message) {
+  g_last_error = message;
+  return code;
+}
+
+int check_launch(const char *what) {
+  hipError_t err = hipGetLastError();
+  if (err != hipSuccess)
+    return fail(XFH_EHIP, std::string(what) + ": launch failed: " + hipGetErrorString(err));
+  return XFH_OK;
+}
+
+static bool float_dtype(int d) { return d == XFH_F32 || d == XFH_BF16; }
+static bool mask_dtype_ok(int d) { return d == XFH_F32 || d == XFH_BF16 || d == XFH_BOOL; }
+static int64_t dsize(int d) { return d == XFH_F32 ? 4 : d == XFH_BF16 ? 2 : 1; }
+
+// Bump allocator over a caller-provided workspace; 256-byte aligned slices.
+struct Carver {
+  char *base;
+  int64_t used = 0, cap;
+  Carver(void *b, int64_t c) : base(static_cast<char *>(b)), cap(c) {}
+  void *take(int64_t bytes) {
+    used = align_up(used, 256);
+    void *p = base ? base + used : nullptr;
+    used += bytes;
+    return p;
+  }
+};
+
+static GemmArgs gemm_args(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
+                          int64_t ldc, int64_t M, int64_t N, int64_t K) {
+  GemmArgs g;
+  std::memset(&g, 0, sizeof(g));
+  g.A = A; g.lda = lda; g.B = B; g.ldb = ldb; g.C = C; g.ldc = ldc;
+  g.M = int(M); g.N = int(N); g.K = int(K);
+  g.epi = XFH_EPI_STORE;
+  return g;
+}
+
+// ------------------------------------------------------------------ triangle multiplication
+struct TriMulPlan {
+  void *normed, *proj, *gate, *left, *right, *contracted, *centered, *gating;
+};
+
+static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int dtype, int out_dtype) {
+  const int64_t es = dsize(dtype), plane = n * n;
+  p.normed = cv.take(plane * c * es);
+  p.proj = cv.take(plane * 2 * c * es);
+  p.gate = cv.take(plane * 2 * c * es);
+  p.left = cv.take(plane * c * es);
+  p.right = cv.take(plane * c * es);
+  p.contracted = cv.take(plane * c * es);
+  p.centered = cv.take(plane * c * es);
+  p.gating = cv.take(plane * c * dsize(out_dtype));
+  return cv.used;
+}
+
+// ------------------------------------------------------------------ grid self-attention
+struct GridPlan {
+  void *normed, *bias, *qkv, *attn;
+};
+
+static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t heads, int dtype) {
+  const int64_t es = dsize(dtype), plane = n * n;
+  p.normed = cv.take(plane * c * es);
+  p.bias = cv.take(plane * heads * es);
+  p.qkv = cv.take(plane * 3 * c * es);
+  p.attn = cv.take(plane * c * es);
+  return cv.used;
+}
+
+}  // namespace xfh
+
+using namespace xfh;
+
+extern "C" {
+
+int xfh_abi_version(void) { return XFH_ABI_VERSION; }
+
+const char *xfh_runtime_info(void) {
+  static char info[256];
+  std::snprintf(info, sizeof(info),
+                "{\"library\": \"xfold_hip\", \"abi\": %d, \"arch\": \"gfx950\", \"hip_version\": %d, "
+                "\"mfma\": [\"16x16x32_bf16\", \"16x16x4_f32\"]}",
+                XFH_ABI_VERSION, HIP_VERSION);
+  return info;
+}
+
+const char *xfh_last_error(void) { return g_last_error.c_str(); }
+
+int xfh_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols, const float *weight,
+                   const float *bias, float eps, void *y, int y_dtype, void *stream) {
+  XFH_REQUIRE(rows >= 0 && cols >= 0, "layer_norm: negative size");
+  XFH_REQUIRE(float_dtype(x_dtype) && float_dtype(y_dtype), "layer_norm: dtypes must be f32/bf16");
+  XFH_REQUIRE(rows == 0 || (x && y), "layer_norm: null tensor");
+  XFH_REQUIRE(eps >= 0.f, "layer_norm: eps must be nonnegative");
+  return layer_norm_rows(x, x_dtype, rows, cols, weight, bias, eps, y, y_dtype, as_stream(stream));
+}
+
+int xfh_adaptive_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols,
+                            const void *scale, const void *shift, int aux_dtype, int64_t cond_rows,
+                            float eps, void *y, int y_dtype, void *stream) {
+  XFH_REQUIRE(rows >= 0 && cols >= 0 && cond_rows > 0, "adaptive_layer_norm: bad size");
+  XFH_REQUIRE(rows == 0 || (x && y && scale && shift), "adaptive_layer_norm: null tensor");
+  XFH_REQUIRE(float_dtype(x_dtype) && float_dtype(y_dtype) && float_dtype(aux_dtype),
+              "adaptive_layer_norm: dtypes must be f32/bf16");
+  return adaptive_layer_norm_rows(x, x_dtype, rows, cols, scale, shift, aux_dtype, cond_rows, eps,
+                                  y, y_dtype, as_stream(stream));
+}
+
+int xfh_linear(const void *x, int64_t ldx, const void *w, const float *bias, int64_t m, int64_t k,
+               int64_t n, int dtype, void *y, int64_t ldy, int y_dtype, int epilogue,
+               const void *aux, int64_t ldaux, int64_t aux_rows, void *stream) {
+  XFH_REQUIRE(m >= 0 && k >= 0 && n >= 0, "linear: negative size");
+  XFH_REQUIRE(m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && k < (int64_t(1) << 31),
+              "linear: sizes must fit in 32 bits");
+  XFH_REQUIRE(float_dtype(dtype) && float_dtype(y_dtype), "linear: dtypes must be f32/bf16");
+  XFH_REQUIRE(epilogue >= XFH_EPI_STORE && epilogue <= XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE,
+              "linear: unknown epilogue");
+  const bool needs_aux = epilogue == XFH_EPI_MUL_SIGMOID_AUX || epilogue == XFH_EPI_SIGMOID_MUL_AUX ||
+                         epilogue == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
+  XFH_REQUIRE(!needs_aux || aux, "linear: epilogue needs aux");
+  XFH_REQUIRE(ldx >= k && ldy >= n && (!aux || ldaux >= n), "linear: leading dims too small");
+  if (m == 0 || n == 0) return XFH_OK;
+  XFH_REQUIRE(x && w && y, "linear: null tensor");
+  GemmArgs g = gemm_args(x, ldx, w, k, y, ldy, m, n, k);
+  g.bias = bias;
+  g.epi = epilogue;
+  g.aux = needs_aux ? aux : nullptr;
+  g.ldaux = ldaux;
+  g.aux_rows = aux_rows;
+  return gemm_nt(g, 1, dtype, y_dtype, false, as_stream(stream));
+}
+
+int64_t xfh_glu_packed_rows(int64_t f) { return 2 * align_up(f, 16); }
+
+int xfh_glu_pack_weight(const void *w, int64_t f, int64_t k, int dtype, void *packed, void *stream) {
+  XFH_REQUIRE(f >= 0 && k >= 0, "glu_pack_weight: negative size");
+  XFH_REQUIRE(float_dtype(dtype), "glu_pack_weight: dtype must be f32/bf16");
+  XFH_REQUIRE((f == 0 || k == 0) || (w && packed), "glu_pack_weight: null tensor");
+  return glu_pack(w, f, k, dtype, packed, as_stream(stream));
+}
+
+int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_t k, int64_t f,
+                          int dtype, void *y, int y_dtype, void *stream) {
+  XFH_REQUIRE(m >= 0 && k >= 0 && f >= 0, "gated_linear_unit: negative size");
+  XFH_REQUIRE(m < (int64_t(1) << 31) && k < (int64_t(1) << 31), "gated_linear_unit: sizes must fit in 32 bits");
+  XFH_REQUIRE(float_dtype(dtype) && float_dtype(y_dtype), "gated_linear_unit: dtypes must be f32/bf16");
+  if (m == 0 || f == 0) return XFH_OK;
+  XFH_REQUIRE(x && w_packed && y, "gated_linear_unit: null tensor");
+  GemmArgs g = gemm_args(x, k, w_packed, k, y, f, m, xfh_glu_packed_rows(f), k);
+  g.glu_f = int(f);
+  return gemm_nt(g, 1, dtype, y_dtype, true, as_stream(stream));
+}
+
+int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
+                              const void *mask, int mask_dtype, const void *bias, int bias_dtype,
+                              void *out, const int64_t *shape, const int64_t *strides, float scale,
+                              void *stream) {
+  XFH_REQUIRE(shape && strides, "dot_product_attention: null shape/strides");
+  XFH_REQUIRE(float_dtype(dtype), "dot_product_attention: dtype must be f32/bf16");
+  XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "dot_product_attention: bad mask dtype");
+  XFH_REQUIRE(!bias || float_dtype(bias_dtype), "dot_product_attention: bias must be f32/bf16");
+  AttentionArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.q = q; a.k = k; a.v = v; a.o = out;
+  a.mask = mask; a.mask_dtype = mask_dtype;
+  a.bias = bias; a.bias_dtype = bias_dtype;
+  a.B = shape[0]; a.H = shape[1]; a.Q = shape[2]; a.K = shape[3]; a.D = shape[4]; a.Dv = shape[5];
+  for (int i = 0; i < 6; ++i) XFH_REQUIRE(shape[i] >= 0, "dot_product_attention: negative size");
+  for (int i = 0; i < 3; ++i) {
+    a.qs[i] = strides[i]; a.ks[i] = strides[3 + i]; a.vs[i] = strides[6 + i]; a.os[i] = strides[9 + i];
+  }
+  for (int i = 0; i < 4; ++i) { a.ms[i] = strides[12 + i]; a.bs[i] = strides[16 + i]; }
+  a.scale = scale;
+  if (a.B * a.H * a.Q * a.Dv == 0) return XFH_OK;
+  XFH_REQUIRE(q && out && (a.K == 0 || (k && v)), "dot_product_attention: null tensor");
+  return attention(a, dtype, as_stream(stream));
+}
+
+int64_t xfh_triangle_multiplication_workspace_size(int64_t n, int64_t c, int dtype) {
+  if (n < 0 || c < 0 || !float_dtype(dtype)) return -1;
+  Carver cv(nullptr, 0);
+  TriMulPlan p;
+  return trimul_carve(cv, p, n, c, dtype, XFH_F32) + 256;
+}
+
+int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *mask, int mask_dtype,
+                                int64_t n, int64_t c, int outgoing, const float *left_w,
+                                const float *left_b, float left_eps, const void *proj_w,
+                                const void *gate_w, const float *center_w, const float *center_b,
+                                float center_eps, const void *out_w, const void *gating_w, int dtype,
+                                void *out, int out_dtype, int accumulate, void *workspace,
+                                int64_t workspace_bytes, void *stream) {
+  XFH_REQUIRE(n >= 0 && c > 0, "triangle_multiplication: bad size");
+  XFH_REQUIRE(float_dtype(pair_dtype) && float_dtype(dtype) && float_dtype(out_dtype),
+              "triangle_multiplication: dtypes must be f32/bf16");
+  XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "triangle_multiplication: bad mask dtype");
+  XFH_REQUIRE(left_eps >= 0.f && center_eps >= 0.f, "triangle_multiplication: eps must be nonnegative");
+  if (n == 0) return XFH_OK;
+  XFH_REQUIRE(n * n < (int64_t(1) << 31), "triangle_multiplication: n*n must fit in 32 bits");
+  XFH_REQUIRE(pair && out && proj_w && gate_w && out_w && gating_w, "triangle_multiplication: null tensor");
+  Carver cv(workspace, workspace_bytes);
+  TriMulPlan p;
+  const int64_t need = trimul_carve(cv, p, n, c, dtype, out_dtype);
+  if (!workspace || need > workspace_bytes)
+    return fail(XFH_EWORKSPACE, "triangle_multiplication: workspace too small (need " +
+                                    std::to_string(need) + " bytes)");
+  hipStream_t s = as_stream(stream);
+  const int64_t plane = n * n;
+  XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, left_w, left_b, left_eps, p.normed, dtype, s));
+  GemmArgs g = gemm_args(p.normed, c, proj_w, c, p.proj, 2 * c, plane, 2 * c, c);
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  g = gemm_args(p.normed, c, gate_w, c, p.gate, 2 * c, plane, 2 * c, c);
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  XFH_TRY(trimul_gate(p.proj, p.gate, dtype, mask, mask_dtype, n, c, outgoing, p.left, p.right, s));
+  // Per-channel contraction: contracted[k] = left[k] right[k]^T, batch = c.
+  g = gemm_args(p.left, n, p.right, n, p.contracted, n, n, n, n);
+  g.sA = plane; g.sB = plane; g.sC = plane;
+  XFH_TRY(gemm_nt(g, c, dtype, dtype, false, s));
+  XFH_TRY(layer_norm_planes(p.contracted, dtype, plane, int(c), center_w, center_b, center_eps,
+                            p.centered, dtype, s));
+  g = gemm_args(p.normed, c, gating_w, c, p.gating, c, plane, c, c);
+  XFH_TRY(gemm_nt(g, 1, dtype, out_dtype, false, s));
+  g = gemm_args(p.centered, c, out_w, c, out, c, plane, c, c);
+  g.aux = p.gating; g.ldaux = c;
+  g.epi = accumulate ? XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE : XFH_EPI_MUL_SIGMOID_AUX;
+  return gemm_nt(g, 1, dtype, out_dtype, false, s);
+}
+
+int64_t xfh_grid_self_attention_workspace_size(int64_t n, int64_t c, int64_t heads, int dtype) {
+  if (n < 0 || c < 0 || heads <= 0 || !float_dtype(dtype)) return -1;
+  Carver cv(nullptr, 0);
+  GridPlan p;
+  return grid_carve(cv, p, n, c, heads, dtype) + 256;
+}
+
+int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, int mask_dtype,
+                            int64_t n, int64_t c, int64_t heads, int transpose, const float *norm_w,
+                            const float *norm_b, float eps, const void *bias_w, const void *q_w,
+                            const void *k_w, const void *v_w, const void *gating_w,
+                            const void *out_w, int dtype, void *out, int out_dtype, int accumulate,
+                            void *workspace, int64_t workspace_bytes, void *stream) {
+  XFH_REQUIRE(n >= 0 && c > 0 && heads > 0 && c % heads == 0, "grid_self_attention: bad size");
+  XFH_REQUIRE(c / heads <= 64, "grid_self_attention: head dim must be <= 64");
+  XFH_REQUIRE(float_dtype(pair_dtype) && float_dtype(dtype) && float_dtype(out_dtype),
+              "grid_self_attention: dtypes must be f32/bf16");
+  XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "grid_self_attention: bad mask dtype");
+  if (n == 0) return XFH_OK;
+  XFH_REQUIRE(n * n < (int64_t(1) << 31), "grid_self_attention: n*n must fit in 32 bits");
+  XFH_REQUIRE(pair && out && bias_w && q_w && k_w && v_w && gating_w && out_w,
+              "grid_self_attention: null tensor");
+  Carver cv(workspace, workspace_bytes);
+  GridPlan p;
+  const int64_t need = grid_carve(cv, p, n, c, heads, dtype);
+  if (!workspace || need > workspace_bytes)
+    return fail(XFH_EWORKSPACE, "grid_self_attention: workspace too small (need " +
+                                    std::to_string(need) + " bytes)");
+  hipStream_t s = as_stream(stream);
+  const int64_t plane = n * n, es = dsize(dtype), dh = c / heads;
+  XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, norm_w, norm_b, eps, p.normed, dtype, s));
+  GemmArgs g = gemm_args(p.normed, c, bias_w, c, p.bias, heads, plane, heads, c);
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  const void *ws[3] = {q_w, k_w, v_w};
+  for (int i = 0; i < 3; ++i) {
+    g = gemm_args(p.normed, c, ws[i], c, static_cast<char *>(p.qkv) + i * c * es, 3 * c, plane, c, c);
+    XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  }
+  // Batch row b, position t of the (optionally transposed) grid lives at pair row
+  // b*n + t (starting node) or t*n + b (ending node); the output keeps pair rows.
+  const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
+  AttentionArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.q = p.qkv;
+  a.k = static_cast<char *>(p.qkv) + c * es;
+  a.v = static_cast<char *>(p.qkv) + 2 * c * es;
+  a.o = p.attn;
+  a.B = n; a.H = heads; a.Q = n; a.K = n; a.D = dh; a.Dv = dh;
+  const int64_t qkv_ld = 3 * c;
+  a.qs[0] = a.ks[0] = a.vs[0] = row_b * qkv_ld;
+  a.qs[1] = a.ks[1] = a.vs[1] = dh;
+  a.qs[2] = a.ks[2] = a.vs[2] = row_t * qkv_ld;
+  a.os[0] = row_b * c; a.os[1] = dh; a.os[2] = row_t * c;
+  a.mask = mask; a.mask_dtype = mask_dtype;
+  a.ms[0] = n; a.ms[1] = 0; a.ms[2] = 0; a.ms[3] = 1;
+  a.bias = p.bias; a.bias_dtype = dtype;
+  a.bs[0] = 0; a.bs[1] = 1; a.bs[2] = n * heads; a.bs[3] = heads;
+  a.scale = 1.0f / std::sqrt(float(dh));
+  XFH_TRY(attention(a, dtype, s));
+  // attn <- sigmoid(LN(z) Wgate^T) * attn, in place.
+  g = gemm_args(p.normed, c, gating_w, c, p.attn, c, plane, c, c);
+  g.epi = XFH_EPI_SIGMOID_MUL_AUX; g.aux = p.attn; g.ldaux = c;
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  g = gemm_args(p.attn, c, out_w, c, out, c, plane, c, c);
+  g.epi = accumulate ? XFH_EPI_ACCUMULATE : XFH_EPI_STORE;
+  return gemm_nt(g, 1, dtype, out_dtype, false, s);
+}
+
+int64_t xfh_transition_workspace_size(int64_t rows, int64_t c, int64_t f, int dtype) {
+  if (rows < 0 || c < 0 || f < 0 || !float_dtype(dtype)) return -1;
+  const int64_t es = dsize(dtype);
+  return align_up(rows * c * es, 256) + align_up(rows * f * es, 256) + 256;
+}
+
+int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t f,
+                   const float *norm_w, const float *norm_b, float eps, const void *w1_packed,
+                   const void *w2, int dtype, void *out, int out_dtype, int accumulate,
+                   void *workspace, int64_t workspace_bytes, void *stream) {
+  XFH_REQUIRE(rows >= 0 && c > 0 && f > 0, "transition: bad size");
+  XFH_REQUIRE(rows < (int64_t(1) << 31), "transition: rows must fit in 32 bits");
+  XFH_REQUIRE(float_dtype(x_dtype) && float_dtype(dtype) && float_dtype(out_dtype),
+              "transition: dtypes must be f32/bf16");
+  if (rows == 0) return XFH_OK;
+  XFH_REQUIRE(x && out && w1_packed && w2, "transition: null tensor");
+  Carver cv(workspace, workspace_bytes);
+  const int64_t es = dsize(dtype);
+  void *normed = cv.take(rows * c * es);
+  void *hidden = cv.take(rows * f * es);
+  if (!workspace || cv.used > workspace_bytes)
+    return fail(XFH_EWORKSPACE, "transition: workspace too small (need " + std::to_string(cv.used) + " bytes)");
+  hipStream_t s = as_stream(stream);
+  XFH_TRY(layer_norm_rows(x, x_dtype, rows, c, norm_w, norm_b, eps, normed, dtype, s));
+  GemmArgs g = gemm_args(normed, c, w1_packed, c, hidden, f, rows, xfh_glu_packed_rows(f), c);
+  g.glu_f = int(f);
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, true, s));
+  g = gemm_args(hidden, f, w2, f, out, c, rows, c, f);
+  g.epi = accumulate ? XFH_EPI_ACCUMULATE : XFH_EPI_STORE;
+  return gemm_nt(g, 1, dtype, out_dtype, false, s);
+}
+
+}  // extern "C"

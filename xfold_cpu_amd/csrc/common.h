@@ -1,0 +1,91 @@
+// Shared device/host helpers for the xfold HIP library (gfx950 / CDNA4 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/xfold_hip.h"
+
+namespace xfh {
+
+typedef __bf16 bf16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(4))) __bf16 bf16x4;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+constexpr int kWave = 64;
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---------------------------------------------------------------- error reporting (host)
+void set_error(const std::string &message);
+int fail(int code, const std::string &message);
+int check_launch(const char *what);
+
+#define XFH_REQUIRE(cond, msg)                                   \
+  do {                                                           \
+    if (!(cond)) return ::xfh::fail(XFH_EINVAL, (msg));          \
+  } while (0)
+
+#define XFH_TRY(expr)                                            \
+  do {                                                           \
+    int _status = (expr);                                        \
+    if (_status != XFH_OK) return _status;                       \
+  } while (0)
+
+inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// ---------------------------------------------------------------- device helpers
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }
+template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; }
+
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+
+// Reads element `i` of a tensor whose dtype is only known at run time (masks, biases).
+__device__ __forceinline__ float load_any(const void *p, int dtype, int64_t i) {
+  if (dtype == XFH_F32) return reinterpret_cast<const float *>(p)[i];
+  if (dtype == XFH_BF16) return static_cast<float>(reinterpret_cast<const bf16 *>(p)[i]);
+  return reinterpret_cast<const uint8_t *>(p)[i] ? 1.0f : 0.0f;
+}
+
+template <typename T> __device__ __forceinline__ T wave_sum(T v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Sum across groups of `width` consecutive lanes (width a power of two <= 64).
+template <int width> __device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// MFMA wrappers. Both keep the 16x16 output layout: lane l holds column l%16 and rows
+// 4*(l/16) + {0,1,2,3}. For bf16 a lane supplies 8 consecutive k of its row (k-group
+// l/16). For fp32 the 16x16x4 instruction takes one k per lane; eight of them consume
+// the same 8-element fragment, slot s of k-group g carrying k = 8g + s. Both operands
+// use the same permutation, so the dot product over the 32-wide k-step is unchanged.
+__device__ __forceinline__ f32x4 mfma16(const bf16x8 &a, const bf16x8 &b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+struct f32x8 { float v[8]; };
+__device__ __forceinline__ f32x4 mfma16(const f32x8 &a, const f32x8 &b, f32x4 c) {
+#pragma unroll
+  for (int s = 0; s < 8; ++s) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a.v[s], b.v[s], c, 0, 0, 0);
+  return c;
+}
+
+template <typename T> struct Frag;
+template <> struct Frag<bf16> { typedef bf16x8 type; };
+template <> struct Frag<float> { typedef f32x8 type; };
+
+}  // namespace xfh

@@ -1,0 +1,51 @@
+// Internal launch interfaces shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include "common.h"
+
+namespace xfh {
+
+struct GemmArgs {
+  const void *A;
+  int64_t lda, sA;          // row stride, batch stride (elements)
+  const void *B;
+  int64_t ldb, sB;
+  void *C;
+  int64_t ldc, sC;
+  const float *bias;        // [N] or null
+  const void *aux;          // epilogue operand in C's dtype, or null
+  int64_t ldaux, sAux, aux_rows;
+  int M, N, K;
+  int epi;                  // XFH_EPI_*
+  int glu_f;                // GLU output features (GLU launches only)
+};
+
+int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s);
+int glu_pack(const void *w, int64_t f, int64_t k, int dtype, void *packed, hipStream_t s);
+
+int layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, const float *w, const float *b,
+                    float eps, void *y, int yd, hipStream_t s);
+int adaptive_layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, const void *scale,
+                             const void *shift, int ad, int64_t cond_rows, float eps, void *y,
+                             int yd, hipStream_t s);
+int layer_norm_planes(const void *x, int xd, int64_t plane, int C, const float *w, const float *b,
+                      float eps, void *y, int yd, hipStream_t s);
+
+struct AttentionArgs {
+  const void *q, *k, *v;
+  void *o;
+  const void *mask;
+  const void *bias;
+  int mask_dtype, bias_dtype;
+  int64_t B, H, Q, K, D, Dv;
+  int64_t qs[3], ks[3], vs[3], os[3];
+  int64_t ms[4], bs[4];
+  float scale;
+};
+int attention(const AttentionArgs &a, int dtype, hipStream_t s);
+
+// Triangle multiplication helpers.
+int trimul_gate(const void *proj, const void *gate, int dtype, const void *mask, int mask_dtype,
+                int64_t n, int64_t c, int outgoing, void *a_out, void *b_out, hipStream_t s);
+
+}  // namespace xfh

@@ -1,0 +1,162 @@
+"""HIP operator wrappers over libxfold_hip.so (tensor checks, dtype resolution, launch).
+
+Each function validates its torch tensors, resolves the compute dtype (CUDA/HIP autocast
+state, as the reference resolves the CPU one in ``xfold/fastnn/native.py:31-43``),
+allocates outputs and workspaces with the PyTorch caching allocator, and enqueues the
+library call on the current stream. None of them computes anything with torch.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from typing import Optional
+
+import torch
+
+from . import native_hip as nh
+
+
+def _out_dtype_for_norm(x: torch.Tensor) -> torch.dtype:
+    # CUDA autocast runs layer_norm in fp32 (its fp32 op list); outside autocast the
+    # output keeps the input dtype, as F.layer_norm does.
+    return torch.float32 if torch.is_autocast_enabled("cuda") else x.dtype
+
+
+def layer_norm(x: torch.Tensor, normalized_shape, weight: Optional[torch.Tensor],
+               bias: Optional[torch.Tensor], eps: float, out_dtype: Optional[torch.dtype] = None,
+               owner: Optional[torch.nn.Module] = None) -> torch.Tensor:
+    """F.layer_norm over the trailing ``normalized_shape`` (``xfold/fastnn/layer_norm.py:56-59``)."""
+    nh.check_gpu_inference(x, weight, bias)
+    if x.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("The 'hip' LayerNorm supports FP32/BF16 inputs.")
+    shape = tuple(normalized_shape) if not isinstance(normalized_shape, int) else (normalized_shape,)
+    if tuple(x.shape[len(x.shape) - len(shape):]) != shape:
+        raise ValueError(f"LayerNorm: input shape {tuple(x.shape)} does not end with {shape}.")
+    cols = 1
+    for s in shape:
+        cols *= s
+    x_c = x.contiguous()
+    rows = x_c.numel() // cols if cols else 0
+    out_dtype = out_dtype or _out_dtype_for_norm(x)
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    w = _fp32(weight, owner, "ln_weight")
+    b = _fp32(bias, owner, "ln_bias")
+    nh.call("xfh_layer_norm", nh.ptr(x_c), nh.dtype_code(x.dtype), rows, cols, nh.ptr(w), nh.ptr(b),
+            float(eps), nh.ptr(y), nh.dtype_code(out_dtype), nh.stream_of(x.device))
+    return y
+
+
+def _fp32(param, owner, name):
+    if param is None:
+        return None
+    if param.dtype == torch.float32 and param.is_contiguous():
+        return param.detach()
+    if owner is not None:
+        return nh.module_cache(owner, name).get(param, torch.float32)
+    return param.detach().to(torch.float32).contiguous()
+
+
+def adaptive_layer_norm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, eps: float,
+                        out_dtype: torch.dtype) -> torch.Tensor:
+    """sigmoid(scale) * LN_noaffine(x) + shift; scale/shift [cond_rows, C] broadcast over
+    leading sample dims (``xfold/nn/diffusion_transformer.py:57-62``)."""
+    cols = x.shape[-1]
+    x_c = x.contiguous()
+    rows = x_c.numel() // cols
+    cond_rows = scale.numel() // cols
+    if scale.shape != shift.shape or rows % max(cond_rows, 1):
+        raise ValueError("adaptive LayerNorm: condition rows must tile the input rows")
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    nh.call("xfh_adaptive_layer_norm", nh.ptr(x_c), nh.dtype_code(x.dtype), rows, cols,
+            nh.ptr(scale), nh.ptr(shift), nh.dtype_code(scale.dtype), cond_rows, float(eps),
+            nh.ptr(y), nh.dtype_code(out_dtype), nh.stream_of(x.device))
+    return y
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], dtype: torch.dtype,
+           out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+           epilogue: int = nh.EPI_STORE, aux: Optional[torch.Tensor] = None,
+           aux_rows: int = 0) -> torch.Tensor:
+    """``out = epilogue(x @ weight^T + bias)`` with weight already in the compute dtype.
+
+    x is cast to the compute dtype if needed (the autocast cast of ``nn.Linear``). ``out``
+    may be given (e.g. the residual stream for the accumulate epilogues).
+    """
+    k = x.shape[-1]
+    n = weight.shape[0]
+    if weight.shape[1] != k:
+        raise ValueError(f"linear: weight {tuple(weight.shape)} does not match input dim {k}")
+    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    m = x_c.numel() // k if k else 0
+    if out is None:
+        out = torch.empty((*x.shape[:-1], n), dtype=out_dtype or dtype, device=x.device)
+    elif not out.is_contiguous() or out.numel() != m * n:
+        raise ValueError("linear: out must be contiguous with matching size")
+    if aux is not None and (aux.dtype != out.dtype or not aux.is_contiguous()):
+        raise ValueError("linear: aux must be contiguous in the output dtype")
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    nh.call("xfh_linear", nh.ptr(x_c), k, nh.ptr(weight), nh.ptr(b), m, k, n, nh.dtype_code(dtype),
+            nh.ptr(out), n, nh.dtype_code(out.dtype), epilogue, nh.ptr(aux), n, aux_rows,
+            nh.stream_of(x.device))
+    return out
+
+
+def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torch.dtype) -> torch.Tensor:
+    """silu(x @ Wg) * (x @ Wv) from the packed weight (``xfold/fastnn/gated_linear_unit.py:103-107``)."""
+    k = x.shape[-1]
+    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    m = x_c.numel() // k if k else 0
+    y = torch.empty((*x.shape[:-1], f), dtype=dtype, device=x.device)
+    nh.call("xfh_gated_linear_unit", nh.ptr(x_c), nh.ptr(packed), m, k, f, nh.dtype_code(dtype),
+            nh.ptr(y), nh.dtype_code(dtype), nh.stream_of(x.device))
+    return y
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
+              bias: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
+              scale: Optional[float] = None) -> torch.Tensor:
+    """4-D [B, H, N, D] strided q/k/v (last dim contiguous); mask/bias broadcast to
+    [B, H, Q, K] per ``xfold/fastnn/attention.py:45-66``."""
+    B, H, Q, D = q.shape
+    K, Dv = k.shape[2], v.shape[3]
+    if k.shape[:2] != (B, H) or v.shape[:3] != (B, H, K) or k.shape[3] != D:
+        raise ValueError("attention: q/k/v shapes do not match")
+    dtype = q.dtype
+    if k.dtype != dtype or v.dtype != dtype:
+        raise ValueError("attention: q/k/v dtypes must match")
+    tensors = []
+    for t in (q, k, v):
+        if t.stride(-1) != 1:
+            t = t.contiguous()
+        tensors.append(t)
+    q, k, v = tensors
+    if out is None:
+        out = torch.empty((B, H, Q, Dv), dtype=dtype, device=q.device)
+    mask_t, mask_code = None, nh.BOOL
+    mask_strides = (0, 0, 0, 0)
+    if mask is not None:
+        if mask.dim() == 1:
+            mask = mask[None, None, None, :]
+        elif mask.dim() == 2:
+            mask = mask[:, None, None, :]
+        if mask.dtype not in (torch.bool, torch.uint8):
+            mask = mask.to(torch.bool)          # the reference's .to(bool) (attention.py:57-61)
+        mask_t = mask.expand(B, H, Q, K)
+        mask_code = nh.BOOL
+        mask_strides = tuple(mask_t.stride())
+    bias_t, bias_code, bias_strides = None, nh.F32, (0, 0, 0, 0)
+    if bias is not None:
+        if bias.dtype not in (torch.float32, torch.bfloat16):
+            bias = bias.to(torch.float32)
+        bias_t = bias.expand(B, H, Q, K)
+        bias_code = nh.dtype_code(bias.dtype)
+        bias_strides = tuple(bias_t.stride())
+    shape = (ctypes.c_int64 * 6)(B, H, Q, K, D, Dv)
+    strides = (ctypes.c_int64 * 20)(
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
+        *mask_strides, *bias_strides)
+    nh.call("xfh_dot_product_attention", nh.ptr(q), nh.ptr(k), nh.ptr(v), nh.dtype_code(dtype),
+            nh.ptr(mask_t), mask_code, nh.ptr(bias_t), bias_code, nh.ptr(out), shape, strides,
+            float(D ** -0.5 if scale is None else scale), nh.stream_of(q.device))
+    return out

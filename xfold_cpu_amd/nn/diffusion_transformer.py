@@ -1,0 +1,262 @@
+"""Diffusion-transformer modules with the reference's constructors, parameter names and
+call signatures (``xfold/nn/diffusion_transformer.py:27-272``), running on the HIP backend:
+AdaptiveLayerNorm, AdaLNZero, DiffusionTransition, SelfAttention (also the Pairformer's
+single-track attention) and DiffusionTransformer.
+
+The ``*_hip`` functions take any module carrying the reference's parameters. Activations
+may carry a leading sample dim ([S, N, c]); conditioning tensors ([N, c_cond]) and pair
+logits ([H, N, N]) are shared by all samples, which is what the reference computes one
+sample at a time.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from ..fastnn import LayerNorm
+from ..fastnn import config as fastnn_config
+from ..fastnn import native_hip as nh
+from ..fastnn import ops
+
+
+def _adaptive_layer_norm(aln: nn.Module, x: torch.Tensor, single_cond: Optional[torch.Tensor],
+                         dtype: torch.dtype, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``AdaptiveLayerNorm.forward`` (``diffusion_transformer.py:51-64``); Linears in
+    ``dtype``, result in ``out_dtype`` (default ``dtype``)."""
+    if (single_cond is None) != (not aln.use_single_cond):
+        raise ValueError("single_cond must be given exactly when use_single_cond is set")
+    out_dtype = out_dtype or dtype
+    if not aln.use_single_cond:
+        ln = aln.layer_norm
+        return ops.layer_norm(x, ln.normalized_shape, ln.weight, ln.bias, ln.eps, out_dtype=out_dtype,
+                              owner=ln)
+    cln = aln.single_cond_layer_norm
+    cond = ops.layer_norm(single_cond, cln.normalized_shape, cln.weight, cln.bias, cln.eps,
+                          out_dtype=dtype, owner=cln)
+    scale = ops.linear(cond, nh.linear_weight(aln, "single_cond_scale", dtype),
+                       aln.single_cond_scale.bias, dtype)
+    shift = ops.linear(cond, nh.linear_weight(aln, "single_cond_bias", dtype), None, dtype)
+    return ops.adaptive_layer_norm(x, scale, shift, aln.layer_norm.eps, out_dtype=out_dtype)
+
+
+def _ada_ln_zero(zero: nn.Module, hidden: torch.Tensor, single_cond: Optional[torch.Tensor],
+                 dtype: torch.dtype, accumulate_into: Optional[torch.Tensor]) -> torch.Tensor:
+    """``AdaLNZero.forward`` (``diffusion_transformer.py:85-95``), optionally added in place."""
+    w = nh.linear_weight(zero, "transition2", dtype)
+    out = accumulate_into
+    out_dtype = out.dtype if out is not None else dtype
+    acc = out is not None
+    if zero.use_single_cond:
+        cond = ops.linear(single_cond, nh.linear_weight(zero, "adaptive_zero_cond", dtype),
+                          zero.adaptive_zero_cond.bias, dtype, out_dtype=out_dtype)
+        epi = nh.EPI_MUL_SIGMOID_AUX_ACCUMULATE if acc else nh.EPI_MUL_SIGMOID_AUX
+        return ops.linear(hidden, w, None, dtype, out=out, out_dtype=out_dtype, epilogue=epi,
+                          aux=cond, aux_rows=cond.numel() // cond.shape[-1])
+    epi = nh.EPI_ACCUMULATE if acc else nh.EPI_STORE
+    return ops.linear(hidden, w, None, dtype, out=out, out_dtype=out_dtype, epilogue=epi)
+
+
+def _check_accumulate(out, x):
+    if out is not None and (not out.is_contiguous() or out.shape != x.shape):
+        raise ValueError("accumulate_into must be a contiguous tensor shaped like x")
+
+
+def diffusion_transition_hip(module: nn.Module, x: torch.Tensor, single_cond=None,
+                             accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``DiffusionTransition.forward`` (``diffusion_transformer.py:124-128``)."""
+    nh.check_gpu_inference(x, single_cond, *module.parameters())
+    dtype = nh.compute_dtype(x, module.transition1.weight)
+    _check_accumulate(accumulate_into, x)
+    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype)
+    f = module.transition1.weight.shape[0] // 2
+    hidden = ops.gated_linear_unit(xn, nh.linear_weight(module, "transition1", dtype, "glu"), f, dtype)
+    return _ada_ln_zero(module.adaptive_zero_init, hidden, single_cond, dtype, accumulate_into)
+
+
+_QKV = ("q_projection", "k_projection", "v_projection")
+
+
+def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.Tensor],
+                       pair_logits: Optional[torch.Tensor] = None,
+                       single_cond: Optional[torch.Tensor] = None,
+                       accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``SelfAttention.forward`` (``diffusion_transformer.py:184-217``) for x [N, c] or
+    [S, N, c]; pair_logits [H, N, N] is the attention bias, mask [N] the key mask."""
+    nh.check_gpu_inference(x, mask, pair_logits, single_cond, *module.parameters())
+    dtype = nh.compute_dtype(x, *(getattr(module, n).weight for n in _QKV + ("gating_query",)))
+    _check_accumulate(accumulate_into, x)
+    if x.dim() not in (2, 3):
+        raise ValueError("SelfAttention expects x [N, c] or [S, N, c]")
+    samples = 1 if x.dim() == 2 else x.shape[0]
+    n, c = x.shape[-2], x.shape[-1]
+    heads = module.num_head
+    d = c // heads
+    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype)
+    w_qkv = nh.fused_linear_weight(module, _QKV, dtype)
+    q_bias = module.q_projection.bias
+    bias_qkv = None
+    if q_bias is not None:
+        bias_qkv = module.__dict__.get("_hip_qkv_bias")
+        key = (q_bias.data_ptr(), q_bias._version) if not q_bias.is_inference() else None
+        if bias_qkv is None or key is None or bias_qkv[0] != key:
+            full = torch.zeros(3 * c, dtype=torch.float32, device=x.device)
+            full[:c] = q_bias.detach().to(torch.float32)
+            bias_qkv = (key, full)
+            if key is not None:
+                module.__dict__["_hip_qkv_bias"] = bias_qkv
+        bias_qkv = bias_qkv[1]
+    qkv = ops.linear(xn, w_qkv, bias_qkv, dtype)                     # [.., N, 3c]
+    qkv = qkv.reshape(samples, n, 3 * c)
+    row = 3 * c
+    views = [torch.as_strided(qkv, (samples, heads, n, d), (n * row, d, row), i * c)
+             for i in range(3)]
+    o = torch.empty((samples, n, c), dtype=dtype, device=x.device)
+    o_view = torch.as_strided(o, (samples, heads, n, d), (n * c, d, c), 0)
+    bias = None
+    if pair_logits is not None:
+        bias = pair_logits if pair_logits.dim() == 4 else pair_logits.unsqueeze(0)
+    ops.attention(views[0], views[1], views[2], mask, bias, out=o_view)
+    ops.linear(xn.reshape(samples, n, c), nh.linear_weight(module, "gating_query", dtype), None, dtype,
+               out=o, epilogue=nh.EPI_SIGMOID_MUL_AUX, aux=o)
+    o = o.reshape(x.shape)
+    return _ada_ln_zero(module.adaptive_zero_init, o, single_cond, dtype, accumulate_into)
+
+
+def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.Tensor,
+                              single_cond: torch.Tensor, pair_cond: torch.Tensor) -> torch.Tensor:
+    """``DiffusionTransformer.forward`` (``diffusion_transformer.py:250-272``), updating
+    ``act`` ([N, c] or [S, N, c], contiguous) in place and returning it."""
+    nh.check_gpu_inference(act, mask, single_cond, pair_cond)
+    if not act.is_contiguous():
+        raise ValueError("DiffusionTransformer (hip) updates act in place; pass a contiguous tensor")
+    dtype = nh.compute_dtype(act, module.pair_logits_projection[0].weight)
+    ln = module.pair_input_layer_norm
+    pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
+                              out_dtype=dtype, owner=ln)
+    heads, size = module.num_head, module.super_block_size
+    for s in range(module.num_super_blocks):
+        weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
+        logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]
+        # 'n s (b h) -> b h n s': block j, head h reads column j*heads + h.
+        for j in range(size):
+            bias = logits[..., j * heads:(j + 1) * heads].permute(2, 0, 1)
+            index = s * size + j
+            self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
+                               accumulate_into=act)
+            diffusion_transition_hip(module.transition_block[index], act, single_cond,
+                                     accumulate_into=act)
+    return act
+
+
+class AdaptiveLayerNorm(nn.Module):
+    def __init__(self, c_x: int, c_single_cond: int, use_single_cond: bool = False) -> None:
+        super().__init__()
+        self.c_x = c_x
+        self.c_single_cond = c_single_cond
+        self.use_single_cond = use_single_cond
+        if use_single_cond:
+            self.layer_norm = LayerNorm(c_x, elementwise_affine=False, bias=False)
+            self.single_cond_layer_norm = LayerNorm(c_single_cond, bias=False)
+            self.single_cond_scale = nn.Linear(c_single_cond, c_x, bias=True)
+            self.single_cond_bias = nn.Linear(c_single_cond, c_x, bias=False)
+        else:
+            self.layer_norm = LayerNorm(c_x)
+
+    def forward(self, x, single_cond=None):
+        _require(fastnn_config.layer_norm_implementation, "layer_norm_implementation")
+        nh.check_gpu_inference(x, single_cond)
+        dtype = nh.compute_dtype(x)
+        # Under CUDA autocast the reference's LayerNorm output is fp32 and so is the
+        # conditioned sum (fp32 * bf16 + bf16); outside autocast it is x's dtype.
+        out_dtype = torch.float32 if torch.is_autocast_enabled("cuda") else x.dtype
+        return _adaptive_layer_norm(self, x, single_cond, dtype, out_dtype)
+
+
+class AdaLNZero(nn.Module):
+    def __init__(self, c_in: int, c_out: int, c_single_cond: int, use_single_cond: bool = False):
+        super().__init__()
+        self.c_in = c_in
+        self.c_out = c_out
+        self.c_single_cond = c_single_cond
+        self.use_single_cond = use_single_cond
+        self.transition2 = nn.Linear(c_in, c_out, bias=False)
+        if use_single_cond:
+            self.adaptive_zero_cond = nn.Linear(c_single_cond, c_out, bias=True)
+
+    def forward(self, x, single_cond=None):
+        dtype = nh.compute_dtype(x, self.transition2.weight)
+        return _ada_ln_zero(self, x, single_cond, dtype, None)
+
+
+def _require(flag_value: str, what: str):
+    if flag_value != fastnn_config.HIP:
+        raise ValueError(f"Unknown {what} for xfold_cpu_amd: {flag_value!r} (only 'hip')")
+
+
+class DiffusionTransition(nn.Module):
+    def __init__(self, c_x: int, c_single_cond: int, num_intermediate_factor: int = 2,
+                 use_single_cond: bool = False) -> None:
+        super().__init__()
+        self.c_x = c_x
+        self.c_single_cond = c_single_cond
+        self.num_intermediate_factor = num_intermediate_factor
+        self.use_single_cond = use_single_cond
+        self.adaptive_layernorm = AdaptiveLayerNorm(c_x, c_single_cond, use_single_cond)
+        self.transition1 = nn.Linear(c_x, 2 * c_x * num_intermediate_factor, bias=False)
+        self.adaptive_zero_init = AdaLNZero(num_intermediate_factor * c_x, c_x, c_single_cond,
+                                            use_single_cond)
+
+    def forward(self, x, single_cond=None):
+        _require(fastnn_config.gated_linear_unit_implementation, "gated_linear_unit_implementation")
+        return diffusion_transition_hip(self, x, single_cond)
+
+
+class SelfAttention(nn.Module):
+    def __init__(self, c_x: int = 768, c_single_cond: int = 384, num_head: int = 16,
+                 use_single_cond: bool = False) -> None:
+        super().__init__()
+        self.c_x = c_x
+        self.c_single_cond = c_single_cond
+        self.num_head = num_head
+        self.qkv_dim = c_x // num_head
+        self.use_single_cond = use_single_cond
+        self.adaptive_layernorm = AdaptiveLayerNorm(c_x, c_single_cond, use_single_cond)
+        self.q_projection = nn.Linear(c_x, c_x, bias=True)
+        self.k_projection = nn.Linear(c_x, c_x, bias=False)
+        self.v_projection = nn.Linear(c_x, c_x, bias=False)
+        self.gating_query = nn.Linear(c_x, c_x, bias=False)
+        self.adaptive_zero_init = AdaLNZero(c_x, c_x, c_single_cond, use_single_cond)
+
+    def forward(self, x, mask, pair_logits=None, single_cond=None):
+        _require(fastnn_config.dot_product_attention_implementation, "dot_product_attention_implementation")
+        return self_attention_hip(self, x, mask, pair_logits, single_cond)
+
+
+class DiffusionTransformer(nn.Module):
+    def __init__(self, c_act: int = 768, c_single_cond: int = 384, c_pair_cond: int = 128,
+                 num_head: int = 16, num_blocks: int = 24, super_block_size: int = 4) -> None:
+        super().__init__()
+        self.c_act = c_act
+        self.c_single_cond = c_single_cond
+        self.c_pair_cond = c_pair_cond
+        self.num_head = num_head
+        self.num_blocks = num_blocks
+        self.super_block_size = super_block_size
+        self.num_super_blocks = num_blocks // super_block_size
+        self.pair_input_layer_norm = LayerNorm(c_pair_cond)
+        self.pair_logits_projection = nn.ModuleList(
+            [nn.Linear(c_pair_cond, super_block_size * num_head, bias=False)
+             for _ in range(self.num_super_blocks)])
+        self.self_attention = nn.ModuleList(
+            [SelfAttention(c_act, c_single_cond, use_single_cond=True) for _ in range(num_blocks)])
+        self.transition_block = nn.ModuleList(
+            [DiffusionTransition(c_act, c_single_cond, use_single_cond=True) for _ in range(num_blocks)])
+
+    def forward(self, act, mask, single_cond, pair_cond):
+        _require(fastnn_config.dot_product_attention_implementation, "dot_product_attention_implementation")
+        _require(fastnn_config.gated_linear_unit_implementation, "gated_linear_unit_implementation")
+        _require(fastnn_config.layer_norm_implementation, "layer_norm_implementation")
+        return diffusion_transformer_hip(self, act, mask, single_cond, pair_cond)

@@ -1,0 +1,82 @@
+"""PairformerBlock with the reference's constructor, submodule names and call signature
+(``xfold/nn/pairformer.py:26-114``), running on the HIP backend.
+
+The block applies its five pair updates in place, each op's final kernel adding its
+result straight into ``pair`` (the residual ``pair += op(pair)`` of ``pairformer.py:96-100``
+without a separate update tensor), then the single track (``pairformer.py:102-113``).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from ..fastnn import LayerNorm
+from ..fastnn import config as fastnn_config
+from ..fastnn import native_hip as nh
+from ..fastnn import ops
+from .attention import GridSelfAttention, grid_self_attention_hip
+from .diffusion_transformer import SelfAttention, self_attention_hip
+from .primitives import Transition, transition_hip
+from .triangle_multiplication import TriangleMultiplication, triangle_multiplication_hip
+
+
+def pair_logits_hip(block: nn.Module, pair: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """``Linear(LN(pair)).permute(2, 0, 1)`` (``pairformer.py:103-106``) as a [H, N, N] view."""
+    norm = block.single_pair_logits_norm
+    normed = ops.layer_norm(pair, norm.normalized_shape, norm.weight, norm.bias, norm.eps,
+                            out_dtype=dtype, owner=norm)
+    logits = ops.linear(normed, nh.linear_weight(block, "single_pair_logits_projection", dtype), None, dtype)
+    return logits.permute(2, 0, 1)
+
+
+def pairformer_block_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.Tensor,
+                         single: Optional[torch.Tensor] = None,
+                         seq_mask: Optional[torch.Tensor] = None):
+    """``PairformerBlock.forward`` (``pairformer.py:77-114``); ``pair`` (and ``single``)
+    must be contiguous and are updated in place, as the reference's ``+=`` does."""
+    if not pair.is_contiguous() or (single is not None and not single.is_contiguous()):
+        raise ValueError("PairformerBlock (hip) updates pair/single in place; pass contiguous tensors")
+    triangle_multiplication_hip(block.triangle_multiplication_outgoing, pair, pair_mask, accumulate_into=pair)
+    triangle_multiplication_hip(block.triangle_multiplication_incoming, pair, pair_mask, accumulate_into=pair)
+    grid_self_attention_hip(block.pair_attention1, pair, pair_mask, accumulate_into=pair)
+    grid_self_attention_hip(block.pair_attention2, pair, pair_mask, accumulate_into=pair)
+    transition_hip(block.pair_transition, pair, accumulate_into=pair)
+    if not block.with_single:
+        return pair
+    dtype = nh.compute_dtype(pair, block.single_pair_logits_projection.weight)
+    logits = pair_logits_hip(block, pair, dtype)
+    self_attention_hip(block.single_attention_, single, seq_mask, logits, None, accumulate_into=single)
+    transition_hip(block.single_transition, single, accumulate_into=single)
+    return pair, single
+
+
+class PairformerBlock(nn.Module):
+    def __init__(self, n_heads: int = 16, c_pair: int = 128, c_single: int = 384,
+                 c_hidden_mul: int = 128, n_heads_pair: int = 4, num_intermediate_factor: int = 4,
+                 with_single: bool = True) -> None:
+        super().__init__()
+        self.n_heads = n_heads
+        self.with_single = with_single
+        self.num_intermediate_factor = num_intermediate_factor
+        self.triangle_multiplication_outgoing = TriangleMultiplication(c_pair=c_pair, _outgoing=True)
+        self.triangle_multiplication_incoming = TriangleMultiplication(c_pair=c_pair, _outgoing=False)
+        self.pair_attention1 = GridSelfAttention(c_pair=c_pair, num_head=n_heads_pair, transpose=False)
+        self.pair_attention2 = GridSelfAttention(c_pair=c_pair, num_head=n_heads_pair, transpose=True)
+        self.pair_transition = Transition(c_x=c_pair, num_intermediate_factor=num_intermediate_factor)
+        self.c_single = c_single
+        if with_single:
+            self.single_pair_logits_norm = LayerNorm(c_pair)
+            self.single_pair_logits_projection = nn.Linear(c_pair, n_heads, bias=False)
+            self.single_attention_ = SelfAttention(c_x=c_single, num_head=n_heads, use_single_cond=False)
+            self.single_transition = Transition(c_x=c_single)
+
+    def forward(self, pair, pair_mask, single=None, seq_mask=None):
+        for name in ("layer_norm_implementation", "dot_product_attention_implementation",
+                     "gated_linear_unit_implementation", "triangle_multiplication_implementation"):
+            if getattr(fastnn_config, name) != fastnn_config.HIP:
+                raise ValueError(f"Unknown {name} for xfold_cpu_amd: "
+                                 f"{getattr(fastnn_config, name)!r} (only 'hip')")
+        return pairformer_block_hip(self, pair, pair_mask, single, seq_mask)
