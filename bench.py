@@ -111,13 +111,13 @@ def grid_attention_roofline(n, device, launches):
     heads, d = 4, 32
     qkv = torch.randn(n, n, 3 * heads * d, device=device, dtype=torch.bfloat16)
     c = heads * d
-    views = [torch.as_strided(qkv, (n, heads, n, d), (n * 3 * c, d, 3 * c), i * c) for i in range(3)]
+    views = [torch.as_strided(qkv, (n, heads, n, d), (n * 3 * c, d, 3 * c, 1), i * c) for i in range(3)]
     bias = torch.randn(n, n, heads, device=device, dtype=torch.bfloat16).permute(2, 0, 1)
     seq = torch.ones(n, device=device)
     seq[-32:] = 0
     mask = seq[:, None] * seq[None, :]
     out = torch.empty(n, n, c, device=device, dtype=torch.bfloat16)
-    o_view = torch.as_strided(out, (n, heads, n, d), (n * c, d, c), 0)
+    o_view = torch.as_strided(out, (n, heads, n, d), (n * c, d, c, 1), 0)
     stream = torch.cuda.current_stream(device)
     with torch.inference_mode():
         for _ in range(3):

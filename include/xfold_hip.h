@@ -92,13 +92,14 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
  * logits in memory). shape = {B, H, Q, K, D, Dv}. strides (elements) =
  *   {q_b, q_h, q_n,  k_b, k_h, k_n,  v_b, v_h, v_n,  o_b, o_h, o_n,
  *    mask_b, mask_h, mask_q, mask_k,  bias_b, bias_h, bias_q, bias_k}
- * (the last dim of q/k/v/out is contiguous; 0 strides broadcast). Semantics of
+ * (the last dim of q/k/v/out is contiguous; 0 strides broadcast). out_dtype may be f32
+ * with bf16 inputs (fp32 accumulation is kept to the store). Semantics of
  * xfold/fastnn/attention.py:45-66: logits = (q*scale) k^T + bias; masked logits := -1e9;
  * softmax over keys; @ v. Replaces `dot_product_attention`
  * (af3_kernels/src/csrc/dot_product_attention.cpp:110-174, bindings.cpp:44-48). */
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
-                              void *out, const int64_t *shape, const int64_t *strides,
+                              void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
                               float scale, void *stream);
 
 /* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).

@@ -170,8 +170,8 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
 
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
-                              void *out, const int64_t *shape, const int64_t *strides, float scale,
-                              void *stream) {
+                              void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
+                              float scale, void *stream) {
   XFH_REQUIRE(shape && strides, "dot_product_attention: null shape/strides");
   XFH_REQUIRE(float_dtype(dtype), "dot_product_attention: dtype must be f32/bf16");
   XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "dot_product_attention: bad mask dtype");
@@ -180,7 +180,8 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   std::memset(&a, 0, sizeof(a));
   a.q = q; a.k = k; a.v = v; a.o = out;
   a.mask = mask; a.mask_dtype = mask_dtype;
-  a.bias = bias; a.bias_dtype = bias_dtype;
+  a.bias = bias; a.bias_dtype = bias_dtype; a.out_dtype = out_dtype;
+  XFH_REQUIRE(float_dtype(out_dtype), "dot_product_attention: out dtype must be f32/bf16");
   a.B = shape[0]; a.H = shape[1]; a.Q = shape[2]; a.K = shape[3]; a.D = shape[4]; a.Dv = shape[5];
   for (int i = 0; i < 6; ++i) XFH_REQUIRE(shape[i] >= 0, "dot_product_attention: negative size");
   for (int i = 0; i < 3; ++i) {
@@ -290,6 +291,7 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   a.k = static_cast<char *>(p.qkv) + c * es;
   a.v = static_cast<char *>(p.qkv) + 2 * c * es;
   a.o = p.attn;
+  a.out_dtype = dtype;
   a.B = n; a.H = heads; a.Q = n; a.K = n; a.D = dh; a.Dv = dh;
   const int64_t qkv_ld = 3 * c;
   a.qs[0] = a.ks[0] = a.vs[0] = row_b * qkv_ld;

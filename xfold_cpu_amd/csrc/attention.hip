@@ -22,7 +22,7 @@ constexpr int KB = 64;    // keys per block
 
 template <typename T> struct AttnSmemPitch { static constexpr int kPad = 16 / sizeof(T); };
 
-template <typename T, int DP, int DVT>
+template <typename T, typename TO, int DP, int DVT>
 __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
   constexpr int kPad = AttnSmemPitch<T>::kPad;
   constexpr int KP = DP + kPad;          // K tile pitch
@@ -173,34 +173,34 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
   l_tot += __shfl_xor(l_tot, 32, 64);
   if (!qvalid) return;
   const float inv = l_tot > 0.f ? 1.0f / l_tot : 0.f;   // no keys at all -> zeros
-  T *op = static_cast<T *>(a.o) + b * a.os[0] + h * a.os[1] + query * a.os[2];
+  TO *op = static_cast<TO *>(a.o) + b * a.os[0] + h * a.os[1] + query * a.os[2];
 #pragma unroll
   for (int t = 0; t < DVT; ++t)
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int64_t d = t * 16 + grp * 4 + e;
-      if (d < a.Dv) op[d] = from_f32<T>(o[t][e] * inv);
+      if (d < a.Dv) op[d] = from_f32<TO>(o[t][e] * inv);
     }
 }
 
-template <typename T, int DP>
+template <typename T, typename TO, int DP>
 int launch_dv(const AttentionArgs &a, hipStream_t s) {
   dim3 grid(ceil_div(a.Q, QB), a.H, a.B);
   const int dvt = int(ceil_div(a.Dv, 16));
   switch (dvt) {
-    case 1: attention_kernel<T, DP, 1><<<grid, 256, 0, s>>>(a); break;
-    case 2: attention_kernel<T, DP, 2><<<grid, 256, 0, s>>>(a); break;
-    case 3: attention_kernel<T, DP, 3><<<grid, 256, 0, s>>>(a); break;
-    case 4: attention_kernel<T, DP, 4><<<grid, 256, 0, s>>>(a); break;
+    case 1: attention_kernel<T, TO, DP, 1><<<grid, 256, 0, s>>>(a); break;
+    case 2: attention_kernel<T, TO, DP, 2><<<grid, 256, 0, s>>>(a); break;
+    case 3: attention_kernel<T, TO, DP, 3><<<grid, 256, 0, s>>>(a); break;
+    case 4: attention_kernel<T, TO, DP, 4><<<grid, 256, 0, s>>>(a); break;
     default: return fail(XFH_EUNSUPPORTED, "attention: value head dim must be <= 64");
   }
   return check_launch("attention");
 }
 
-template <typename T>
+template <typename T, typename TO>
 int launch_typed(const AttentionArgs &a, hipStream_t s) {
-  if (a.D <= 32) return launch_dv<T, 32>(a, s);
-  if (a.D <= 64) return launch_dv<T, 64>(a, s);
+  if (a.D <= 32) return launch_dv<T, TO, 32>(a, s);
+  if (a.D <= 64) return launch_dv<T, TO, 64>(a, s);
   return fail(XFH_EUNSUPPORTED, "attention: head dim must be <= 64");
 }
 
@@ -209,9 +209,10 @@ int launch_typed(const AttentionArgs &a, hipStream_t s) {
 int attention(const AttentionArgs &a, int dtype, hipStream_t s) {
   if (a.B == 0 || a.H == 0 || a.Q == 0 || a.Dv == 0) return XFH_OK;
   if (a.H > 65535 || a.B > 65535) return fail(XFH_EUNSUPPORTED, "attention: B and H must be <= 65535");
-  if (dtype == XFH_BF16) return launch_typed<bf16>(a, s);
-  if (dtype == XFH_F32) return launch_typed<float>(a, s);
-  return fail(XFH_EUNSUPPORTED, "attention: dtype must be f32 or bf16");
+  if (dtype == XFH_BF16 && a.out_dtype == XFH_BF16) return launch_typed<bf16, bf16>(a, s);
+  if (dtype == XFH_BF16 && a.out_dtype == XFH_F32) return launch_typed<bf16, float>(a, s);
+  if (dtype == XFH_F32 && a.out_dtype == XFH_F32) return launch_typed<float, float>(a, s);
+  return fail(XFH_EUNSUPPORTED, "attention: dtypes must be bf16->bf16, bf16->f32 or f32->f32");
 }
 
 }  // namespace xfh

@@ -36,7 +36,7 @@ struct AttentionArgs {
   void *o;
   const void *mask;
   const void *bias;
-  int mask_dtype, bias_dtype;
+  int mask_dtype, bias_dtype, out_dtype;
   int64_t B, H, Q, K, D, Dv;
   int64_t qs[3], ks[3], vs[3], os[3];
   int64_t ms[4], bs[4];

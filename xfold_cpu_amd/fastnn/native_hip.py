@@ -47,7 +47,7 @@ SIGNATURES = {
     "xfh_glu_packed_rows": (_i64, [_i64]),
     "xfh_glu_pack_weight": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "xfh_gated_linear_unit": (_i, [_p, _p, _i64, _i64, _i64, _i, _p, _i, _p]),
-    "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _pi64, _pi64, _f, _p]),
+    "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _pi64, _pi64, _f, _p]),
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
     "xfh_triangle_multiplication": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,
                                          _f, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),

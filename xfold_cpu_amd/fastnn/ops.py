@@ -101,20 +101,21 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], 
     return out
 
 
-def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torch.dtype) -> torch.Tensor:
+def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torch.dtype,
+                      out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """silu(x @ Wg) * (x @ Wv) from the packed weight (``xfold/fastnn/gated_linear_unit.py:103-107``)."""
     k = x.shape[-1]
     x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
     m = x_c.numel() // k if k else 0
-    y = torch.empty((*x.shape[:-1], f), dtype=dtype, device=x.device)
+    y = torch.empty((*x.shape[:-1], f), dtype=out_dtype or dtype, device=x.device)
     nh.call("xfh_gated_linear_unit", nh.ptr(x_c), nh.ptr(packed), m, k, f, nh.dtype_code(dtype),
-            nh.ptr(y), nh.dtype_code(dtype), nh.stream_of(x.device))
+            nh.ptr(y), nh.dtype_code(y.dtype), nh.stream_of(x.device))
     return y
 
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
               bias: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
-              scale: Optional[float] = None) -> torch.Tensor:
+              scale: Optional[float] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """4-D [B, H, N, D] strided q/k/v (last dim contiguous); mask/bias broadcast to
     [B, H, Q, K] per ``xfold/fastnn/attention.py:45-66``."""
     B, H, Q, D = q.shape
@@ -131,7 +132,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
         tensors.append(t)
     q, k, v = tensors
     if out is None:
-        out = torch.empty((B, H, Q, Dv), dtype=dtype, device=q.device)
+        out = torch.empty((B, H, Q, Dv), dtype=out_dtype or dtype, device=q.device)
+    if out.stride(-1) != 1:
+        raise ValueError("attention: out's last dim must be contiguous")
     mask_t, mask_code = None, nh.BOOL
     mask_strides = (0, 0, 0, 0)
     if mask is not None:
@@ -157,6 +160,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
         *mask_strides, *bias_strides)
     nh.call("xfh_dot_product_attention", nh.ptr(q), nh.ptr(k), nh.ptr(v), nh.dtype_code(dtype),
-            nh.ptr(mask_t), mask_code, nh.ptr(bias_t), bias_code, nh.ptr(out), shape, strides,
+            nh.ptr(mask_t), mask_code, nh.ptr(bias_t), bias_code, nh.ptr(out), nh.dtype_code(out.dtype),
+            shape, strides,
             float(D ** -0.5 if scale is None else scale), nh.stream_of(q.device))
     return out

@@ -111,10 +111,10 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     qkv = ops.linear(xn, w_qkv, bias_qkv, dtype)                     # [.., N, 3c]
     qkv = qkv.reshape(samples, n, 3 * c)
     row = 3 * c
-    views = [torch.as_strided(qkv, (samples, heads, n, d), (n * row, d, row), i * c)
+    views = [torch.as_strided(qkv, (samples, heads, n, d), (n * row, d, row, 1), i * c)
              for i in range(3)]
     o = torch.empty((samples, n, c), dtype=dtype, device=x.device)
-    o_view = torch.as_strided(o, (samples, heads, n, d), (n * c, d, c), 0)
+    o_view = torch.as_strided(o, (samples, heads, n, d), (n * c, d, c, 1), 0)
     bias = None
     if pair_logits is not None:
         bias = pair_logits if pair_logits.dim() == 4 else pair_logits.unsqueeze(0)
