@@ -1,0 +1,67 @@
+"""The error floor of bf16-operand matrix arithmetic (test infrastructure only).
+
+Each function re-evaluates a reference operator in float64 with ONLY the operands of its
+matrix products rounded to bf16 (activations and weights entering a matmul, attention
+probabilities and values), accumulating in float64 and keeping every other step exact.
+No implementation that feeds bf16 operands to matrix cores can be systematically more
+accurate; the distance of this result from the exact (float64) operator is the floor
+against which the HIP bf16 path is judged.
+
+Follows the same reference lines as ``oracle.restatement``:
+  triangle_multiplication   xfold/nn/triangle_multiplication.py:71-105
+  grid_self_attention       xfold/nn/attention.py:61-105, xfold/fastnn/attention.py:45-66
+  transition                xfold/nn/primitives.py:33-37
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from . import restatement as R
+
+
+def _r(t: torch.Tensor) -> torch.Tensor:
+    return t.to(torch.bfloat16).to(torch.float64)
+
+
+def _lin(x, w):
+    return _r(x) @ _r(w).T
+
+
+def _ln(x, m):
+    w = None if m.weight is None else m.weight.double()
+    b = None if m.bias is None else m.bias.double()
+    return F.layer_norm(x, (x.shape[-1],), w, b, m.eps)
+
+
+def triangle_multiplication(m, pair, mask):
+    x = _ln(pair.double(), m.left_norm_input)
+    p = _lin(x, m.projection.weight).permute(2, 0, 1)
+    if mask is not None:
+        p = p * mask.double()[None]
+    p = p * torch.sigmoid(_lin(x, m.gate.weight).permute(2, 0, 1))
+    p = p.reshape(m.c_pair, 2, *p.shape[1:])
+    out = torch.einsum(m.equation, _r(p[:, 0]), _r(p[:, 1])).permute(1, 2, 0)
+    out = _lin(_ln(out, m.center_norm), m.output_projection.weight)
+    return out * torch.sigmoid(_lin(x, m.gating_linear.weight))
+
+
+def grid_self_attention(m, pair, mask):
+    x = _ln(pair.double(), m.act_norm)
+    bias = _lin(x, m.pair_bias_projection.weight).permute(2, 0, 1)
+    if m.transpose:
+        x = x.permute(1, 0, 2)
+    q, k, v = (R._heads_first(_lin(x, getattr(m, n).weight), m.num_head)
+               for n in ("q_projection", "k_projection", "v_projection"))
+    logits = _r(q * q.shape[-1] ** -0.5) @ _r(k).transpose(-1, -2) + bias
+    logits = logits.masked_fill(~mask.bool()[:, None, None, :], -1e9)
+    o = R._heads_last(_r(torch.softmax(logits, -1)) @ _r(v))
+    o = _lin(o * torch.sigmoid(_lin(x, m.gating_query.weight)), m.output_projection.weight)
+    return o.permute(1, 0, 2) if m.transpose else o
+
+
+def transition(m, x):
+    x = _ln(x.double(), m.input_layer_norm)
+    gate, value = _lin(x, m.transition1.weight).chunk(2, dim=-1)
+    return _lin(F.silu(gate) * value, m.transition2.weight)

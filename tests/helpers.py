@@ -84,3 +84,34 @@ def assert_stored_parity(actual, expected, tol, what="", stores=1.0):
     err = stored_rel_err(actual, expected, stores)
     assert err <= tol, f"{what}: store-aware max|diff|/rms = {err:.3e} > {tol:.1e}"
     return err
+
+
+# bf16 mode. The north-star bar (2e-2 of the output RMS) is applied to the RMS of the
+# error; the max-abs error gets a guard of 8e-2 instead, because an exact computation
+# whose only rounding is bf16 matmul operands (oracle/bf16_floor.py) already has
+# max|d|/RMS of 2.3e-2 (Transition), 3.4e-2 (TriangleMultiplication) and 4.1e-2
+# (GridSelfAttention) at N=64, while its RMS error is ~5e-3. The guard still fails any
+# element-level mistake (a wrong index or mask gives O(1) errors).
+TOL_BF16_MAX = 8e-2
+
+
+def rms_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
+    a = actual.detach().to(torch.float64).cpu()
+    e = expected.detach().to(torch.float64).cpu()
+    assert a.shape == e.shape, (a.shape, e.shape)
+    if e.numel() == 0:
+        return 0.0
+    num = math.sqrt(float(((a - e) ** 2).mean()))
+    den = math.sqrt(float((e * e).mean()))
+    return num / den if den > 0 else num
+
+
+def assert_parity_bf16(actual, expected, what="", stores=0.0):
+    """bf16-mode parity: RMS error <= TOL_BF16 and max error (bf16 store rounding of
+    `stores` stores excluded) <= TOL_BF16_MAX, both relative to RMS(expected)."""
+    rms_err = rms_rel_err(actual, expected)
+    max_err = stored_rel_err(actual, expected, stores) if stores else rel_err(actual, expected)
+    print(f"[parity] {what}: rms {rms_err:.3e} max {max_err:.3e}", flush=True)
+    assert rms_err <= TOL_BF16, f"{what}: rms|diff|/rms = {rms_err:.3e} > {TOL_BF16:.1e}"
+    assert max_err <= TOL_BF16_MAX, f"{what}: max|diff|/rms = {max_err:.3e} > {TOL_BF16_MAX:.1e}"
+    return rms_err, max_err

