@@ -38,7 +38,6 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--kernel-launches", type=int, default=20)
     return p.parse_args()
 
 
@@ -101,40 +100,33 @@ def build_workload(cfg_name, device):
     return step, 1, workload, cfg
 
 
-def grid_attention_roofline(n, device, launches):
-    """Times the dominant kernel (triangle attention core: B=N rows, 4 heads x 32, N x N,
-    pair bias + 2-D mask) with HIP events on the stream it is launched on."""
+def kernel_roofline(step, n, steps):
+    """Average duration of the dominant kernel (triangle attention core: B=N rows, 4 heads
+    x 32, N x N keys, pair bias and 2-D key mask) inside the block workload, from HIP events
+    the library records around each launch on the launch stream."""
     import torch
-    from xfold_cpu_amd.fastnn import ops
+    from xfold_cpu_amd.fastnn import native_hip
 
-    torch.manual_seed(0)
+    name = "grid_attention"
+    native_hip.kernel_timing_read(name)               # drop anything recorded earlier
+    native_hip.set_kernel_timing(True)
+    try:
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        native_hip.set_kernel_timing(False)
+    total_ms, launches = native_hip.kernel_timing_read(name)
+    if launches == 0:
+        return None
+    ms = total_ms / launches
     heads, d = 4, 32
-    qkv = torch.randn(n, n, 3 * heads * d, device=device, dtype=torch.bfloat16)
-    c = heads * d
-    views = [torch.as_strided(qkv, (n, heads, n, d), (n * 3 * c, d, 3 * c, 1), i * c) for i in range(3)]
-    bias = torch.randn(n, n, heads, device=device, dtype=torch.bfloat16).permute(2, 0, 1)
-    seq = torch.ones(n, device=device)
-    seq[-32:] = 0
-    mask = seq[:, None] * seq[None, :]
-    out = torch.empty(n, n, c, device=device, dtype=torch.bfloat16)
-    o_view = torch.as_strided(out, (n, heads, n, d), (n * c, d, c, 1), 0)
-    stream = torch.cuda.current_stream(device)
-    with torch.inference_mode():
-        for _ in range(3):
-            ops.attention(*views, mask, bias, out=o_view)
-        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        for _ in range(launches):
-            ops.attention(*views, mask, bias, out=o_view)
-        stop.record(stream)
-        stop.synchronize()
-    ms = start.elapsed_time(stop) / launches
-    flops = 4.0 * n * heads * n * n * d            # QK^T + PV, 2 flops per MAC
+    flops = 4.0 * n * heads * n * n * d            # Q.K^T and P.V over all N^3 logits
     achieved = flops / (ms * 1e-3) / 1e12
-    return {"kernel": "attention_kernel (triangle attention core)", "bound": "mfma",
+    return {"kernel": "grid_attention_kernel (triangle attention core)", "bound": "mfma",
             "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
-            "avg_launch_ms": round(ms, 4), "flops_per_launch": flops,
+            "avg_launch_ms": round(ms, 4), "launches": launches, "flops_per_launch": flops,
             "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}
 
 
@@ -206,7 +198,7 @@ def main():
 
     roof = None
     if cfg["kind"] != "diffusion":
-        roof = grid_attention_roofline(cfg["n"], device, args.kernel_launches)
+        roof = kernel_roofline(step, cfg["n"], max(1, min(args.steps, 5)))
         log(f"roofline: {roof}")
     base = None
     if not args.no_cpu_baseline:

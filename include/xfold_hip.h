@@ -52,6 +52,13 @@ const char *xfh_runtime_info(void);
  * TORCH_CHECK -> RuntimeError path of the pybind11 module (af3_kernels/src/csrc/tools.cpp:20-28). */
 const char *xfh_last_error(void);
 
+/* Opt-in timing of the library's dominant kernels (no reference counterpart; used by the
+ * benchmark): while enabled, launches of the named kernels ("grid_attention", ...) are
+ * bracketed by HIP events on their stream. xfh_kernel_timing_read waits for, sums and
+ * releases the recorded intervals of one kernel name. */
+void xfh_set_kernel_timing(int enable);
+int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches);
+
 /* LayerNorm over the last dim of a contiguous [rows, cols] tensor; fp32 statistics.
  * Replaces the LayerNorm backends of xfold/fastnn/layer_norm.py:55-81 (torch/triton/ipex). */
 int xfh_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols,

@@ -1,8 +1,11 @@
 // C ABI of libxfold_hip.so: validation, workspace carving and kernel sequencing.
 // Declarations and their reference counterparts are in include/xfold_hip.h.
+#include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
+#include <vector>
 
 #include "common.h"
 #include "kernels.h"
@@ -23,6 +26,34 @@ int check_launch(const char *what) {
   if (err != hipSuccess)
     return fail(XFH_EHIP, std::string(what) + ": launch failed: " + hipGetErrorString(err));
   return XFH_OK;
+}
+
+// ------------------------------------------------------------------ kernel timing
+namespace {
+struct TimedEvent {
+  std::string name;
+  hipEvent_t start, stop;
+};
+std::mutex g_timing_mutex;
+bool g_timing_enabled = false;
+std::vector<TimedEvent> g_timed;
+}  // namespace
+
+KernelTimer::KernelTimer(const char *name, hipStream_t stream) : name_(name), stream_(stream) {
+  if (!g_timing_enabled) return;
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  hipEventRecord(e, stream_);
+  start_ = e;
+}
+
+KernelTimer::~KernelTimer() {
+  if (!start_) return;
+  hipEvent_t e;
+  if (hipEventCreate(&e) != hipSuccess) return;
+  hipEventRecord(e, stream_);
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  g_timed.push_back({name_, static_cast<hipEvent_t>(start_), e});
 }
 
 static bool float_dtype(int d) { return d == XFH_F32 || d == XFH_BF16; }
@@ -73,7 +104,15 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
 // ------------------------------------------------------------------ grid self-attention
 struct GridPlan {
   void *normed, *bias, *qkv, *attn;
+  // fast bf16 path (head dim 32)
+  void *qh, *kh, *vt;
+  float *bias_t;
+  uint64_t *maskbits;
 };
+
+static bool grid_fast_path(int64_t c, int64_t heads, int dtype) {
+  return dtype == XFH_BF16 && c / heads == 32 && c % heads == 0;
+}
 
 static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t heads, int dtype) {
   const int64_t es = dsize(dtype), plane = n * n;
@@ -81,6 +120,17 @@ static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t
   p.bias = cv.take(plane * heads * es);
   p.qkv = cv.take(plane * 3 * c * es);
   p.attn = cv.take(plane * c * es);
+  p.qh = p.kh = p.vt = nullptr;
+  p.bias_t = nullptr;
+  p.maskbits = nullptr;
+  if (grid_fast_path(c, heads, dtype)) {
+    const int64_t npad = grid_attention_pad(n);
+    p.qh = cv.take(plane * c * es);
+    p.kh = cv.take(plane * c * es);
+    p.vt = cv.take(n * c * npad * es);
+    p.bias_t = static_cast<float *>(cv.take(heads * n * npad * 4));
+    p.maskbits = static_cast<uint64_t *>(cv.take(n * (npad / 64) * 8));
+  }
   return cv.used;
 }
 
@@ -102,6 +152,37 @@ const char *xfh_runtime_info(void) {
 }
 
 const char *xfh_last_error(void) { return g_last_error.c_str(); }
+
+void xfh_set_kernel_timing(int enable) {
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  g_timing_enabled = enable != 0;
+}
+
+int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches) {
+  XFH_REQUIRE(name && total_ms && launches, "kernel_timing_read: null argument");
+  std::lock_guard<std::mutex> lock(g_timing_mutex);
+  double total = 0.0;
+  int64_t count = 0;
+  std::vector<TimedEvent> keep;
+  for (auto &t : g_timed) {
+    if (t.name != name) {
+      keep.push_back(t);
+      continue;
+    }
+    if (hipEventSynchronize(t.stop) != hipSuccess) return fail(XFH_EHIP, "kernel_timing_read: sync failed");
+    float ms = 0.f;
+    if (hipEventElapsedTime(&ms, t.start, t.stop) != hipSuccess)
+      return fail(XFH_EHIP, "kernel_timing_read: elapsed time failed");
+    total += ms;
+    ++count;
+    hipEventDestroy(t.start);
+    hipEventDestroy(t.stop);
+  }
+  g_timed.swap(keep);
+  *total_ms = total;
+  *launches = count;
+  return XFH_OK;
+}
 
 int xfh_layer_norm(const void *x, int x_dtype, int64_t rows, int64_t cols, const float *weight,
                    const float *bias, float eps, void *y, int y_dtype, void *stream) {
@@ -285,6 +366,24 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   // Batch row b, position t of the (optionally transposed) grid lives at pair row
   // b*n + t (starting node) or t*n + b (ending node); the output keeps pair rows.
   const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
+  if (grid_fast_path(c, heads, dtype)) {
+    const float scale = 1.0f / std::sqrt(float(dh));
+    XFH_TRY(grid_attention_prepare(p.qkv, p.bias, mask, mask_dtype, n, int(heads), transpose, scale,
+                                   p.qh, p.kh, p.vt, p.bias_t, p.maskbits, s));
+    GridAttentionArgs ga;
+    ga.q = static_cast<const bf16 *>(p.qh);
+    ga.k = static_cast<const bf16 *>(p.kh);
+    ga.vt = static_cast<const bf16 *>(p.vt);
+    ga.bias = p.bias_t;
+    ga.maskbits = p.maskbits;
+    ga.out = static_cast<bf16 *>(p.attn);
+    ga.osb = row_b * c;
+    ga.ost = row_t * c;
+    ga.B = int(n); ga.H = int(heads); ga.N = int(n);
+    ga.Npad = int(grid_attention_pad(n));
+    ga.Nblk = ga.Npad / 64;
+    XFH_TRY(grid_attention(ga, s));
+  } else {
   AttentionArgs a;
   std::memset(&a, 0, sizeof(a));
   a.q = p.qkv;
@@ -304,6 +403,7 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   a.bs[0] = 0; a.bs[1] = 1; a.bs[2] = n * heads; a.bs[3] = heads;
   a.scale = 1.0f / std::sqrt(float(dh));
   XFH_TRY(attention(a, dtype, s));
+  }
   // attn <- sigmoid(LN(z) Wgate^T) * attn, in place.
   g = gemm_args(p.normed, c, gating_w, c, p.attn, c, plane, c, c);
   g.epi = XFH_EPI_SIGMOID_MUL_AUX; g.aux = p.attn; g.ldaux = c;

@@ -36,6 +36,18 @@ int check_launch(const char *what);
   } while (0)
 
 inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Opt-in per-kernel timing (xfh_set_kernel_timing): when enabled, a KernelTimer brackets a
+// launch with HIP events recorded on the launch stream.
+class KernelTimer {
+ public:
+  KernelTimer(const char *name, hipStream_t stream);
+  ~KernelTimer();
+ private:
+  const char *name_;
+  hipStream_t stream_;
+  void *start_ = nullptr;
+};
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 

@@ -44,6 +44,21 @@ struct AttentionArgs {
 };
 int attention(const AttentionArgs &a, int dtype, hipStream_t s);
 
+// Triangle (grid) attention, bf16, head dim 32 (grid_attention.hip).
+struct GridAttentionArgs {
+  const bf16 *q, *k, *vt;
+  const float *bias;
+  const uint64_t *maskbits;
+  bf16 *out;
+  int64_t osb, ost;          // out element (b, t, h, d) at out[b*osb + t*ost + h*32 + d]
+  int B, H, N, Npad, Nblk;
+};
+int64_t grid_attention_pad(int64_t n);
+int grid_attention_prepare(const void *qkv, const void *bias_lin, const void *mask, int mask_dtype,
+                           int64_t n, int heads, int transpose, float scale, void *qh, void *kh,
+                           void *vt, float *bias, uint64_t *maskbits, hipStream_t s);
+int grid_attention(const GridAttentionArgs &a, hipStream_t s);
+
 // Triangle multiplication helpers.
 int trimul_gate(const void *proj, const void *gate, int dtype, const void *mask, int mask_dtype,
                 int64_t n, int64_t c, int outgoing, void *a_out, void *b_out, hipStream_t s);

@@ -41,6 +41,8 @@ SIGNATURES = {
     "xfh_abi_version": (_i, []),
     "xfh_runtime_info": (ctypes.c_char_p, []),
     "xfh_last_error": (ctypes.c_char_p, []),
+    "xfh_set_kernel_timing": (None, [_i]),
+    "xfh_kernel_timing_read": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _pi64]),
     "xfh_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _p]),
     "xfh_adaptive_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _i64, _f, _p, _i, _p]),
     "xfh_linear": (_i, [_p, _i64, _p, _p, _i64, _i64, _i64, _i, _p, _i64, _i, _i, _p, _i64, _i64, _p]),
@@ -93,6 +95,17 @@ def call(name: str, *args) -> None:
         if status in (1, 2):
             raise ValueError(f"{name}: {message}")
         raise HipBackendError(f"{name} failed ({status}): {message}")
+
+
+def set_kernel_timing(enable: bool) -> None:
+    load_library().xfh_set_kernel_timing(int(enable))
+
+
+def kernel_timing_read(name: str):
+    """(total milliseconds, launches) recorded for ``name`` since the last read."""
+    total, count = ctypes.c_double(), ctypes.c_int64()
+    call("xfh_kernel_timing_read", name.encode(), ctypes.byref(total), ctypes.byref(count))
+    return total.value, count.value
 
 
 def runtime_info() -> str:
