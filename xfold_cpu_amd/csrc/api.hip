@@ -85,11 +85,21 @@ static GemmArgs gemm_args(const void *A, int64_t lda, const void *B, int64_t ldb
 
 // ------------------------------------------------------------------ triangle multiplication
 struct TriMulPlan {
-  void *normed, *proj, *gate, *left, *right, *contracted, *centered, *gating;
+  void *normed, *proj, *gate, *left, *right, *contracted, *centered, *gating, *packed;
 };
+
+static bool trimul_fast_path(int64_t c, int dtype) { return dtype == XFH_BF16 && c == 128; }
 
 static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int dtype, int out_dtype) {
   const int64_t es = dsize(dtype), plane = n * n;
+  std::memset(&p, 0, sizeof(p));
+  if (trimul_fast_path(c, dtype)) {
+    p.packed = cv.take(4 * c * c * es);
+    p.left = cv.take(plane * c * es);
+    p.right = cv.take(plane * c * es);
+    p.contracted = cv.take(plane * c * es);
+    return cv.used;
+  }
   p.normed = cv.take(plane * c * es);
   p.proj = cv.take(plane * 2 * c * es);
   p.gate = cv.take(plane * 2 * c * es);
@@ -305,6 +315,29 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
                                     std::to_string(need) + " bytes)");
   hipStream_t s = as_stream(stream);
   const int64_t plane = n * n;
+  if (trimul_fast_path(c, dtype)) {
+    XFH_TRY(trimul_pack(proj_w, gate_w, int(c), p.packed, s));
+    TriProjectArgs pa;
+    pa.pair = pair; pa.mask = mask; pa.mask_dtype = mask_dtype;
+    pa.ln_w = left_w; pa.ln_b = left_b; pa.eps = left_eps;
+    pa.w_packed = static_cast<const bf16 *>(p.packed);
+    pa.left = static_cast<bf16 *>(p.left); pa.right = static_cast<bf16 *>(p.right);
+    pa.n = int(n); pa.outgoing = outgoing;
+    XFH_TRY(trimul_project(pa, pair_dtype, s));
+    GemmArgs g = gemm_args(p.left, n, p.right, n, p.contracted, n, n, n, n);
+    g.sA = plane; g.sB = plane; g.sC = plane;
+    {
+      KernelTimer timer("trimul_contract", s);
+      XFH_TRY(gemm_nt(g, c, dtype, dtype, false, s));
+    }
+    TriOutputArgs oa;
+    oa.pair = pair; oa.contracted = static_cast<const bf16 *>(p.contracted);
+    oa.ln_in_w = left_w; oa.ln_in_b = left_b; oa.eps_in = left_eps;
+    oa.ln_c_w = center_w; oa.ln_c_b = center_b; oa.eps_c = center_eps;
+    oa.w_gating = static_cast<const bf16 *>(gating_w); oa.w_out = static_cast<const bf16 *>(out_w);
+    oa.out = out; oa.accumulate = accumulate; oa.n = int(n);
+    return trimul_output(oa, pair_dtype, out_dtype, s);
+  }
   XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, left_w, left_b, left_eps, p.normed, dtype, s));
   GemmArgs g = gemm_args(p.normed, c, proj_w, c, p.proj, 2 * c, plane, 2 * c, c);
   XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));

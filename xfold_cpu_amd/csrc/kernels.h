@@ -59,6 +59,32 @@ int grid_attention_prepare(const void *qkv, const void *bias_lin, const void *ma
                            void *vt, float *bias, uint64_t *maskbits, hipStream_t s);
 int grid_attention(const GridAttentionArgs &a, hipStream_t s);
 
+// Fused triangle multiplication, bf16 compute, c = 128 (trimul_fused.hip).
+struct TriProjectArgs {
+  const void *pair;
+  const void *mask;
+  int mask_dtype;
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w_packed;      // [4c][c], see trimul_pack
+  bf16 *left, *right;        // [c][n][n] contraction operands
+  int n, outgoing;
+};
+struct TriOutputArgs {
+  const void *pair;
+  const bf16 *contracted;    // [c][n][n]
+  const float *ln_in_w, *ln_in_b;
+  float eps_in;
+  const float *ln_c_w, *ln_c_b;
+  float eps_c;
+  const bf16 *w_gating, *w_out;
+  void *out;
+  int accumulate, n;
+};
+int trimul_pack(const void *proj, const void *gate, int c, void *packed, hipStream_t s);
+int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s);
+int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
+
 // Triangle multiplication helpers.
 int trimul_gate(const void *proj, const void *gate, int dtype, const void *mask, int mask_dtype,
                 int64_t n, int64_t c, int outgoing, void *a_out, void *b_out, hipStream_t s);
