@@ -58,8 +58,22 @@ template <> __device__ __forceinline__ float to_f32<float>(float v) { return v; 
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return static_cast<T>(v); }
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 
-__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
-__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+// sigmoid / SiLU with the hardware reciprocal (1 ulp) instead of an IEEE division.
+__device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// DPP lane exchange inside a 16-lane row (no LDS traffic).
+template <int CTRL> __device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+// Sum over each row of 16 lanes: xor 1, xor 2 (quad permutes), then half-row and row mirrors.
+__device__ __forceinline__ float row16_sum(float v) {
+  v += dpp_f32<0xB1>(v);    // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(v);    // quad_perm [2,3,0,1]
+  v += dpp_f32<0x141>(v);   // row_half_mirror
+  v += dpp_f32<0x140>(v);   // row_mirror
+  return v;
+}
 
 // Reads element `i` of a tensor whose dtype is only known at run time (masks, biases).
 __device__ __forceinline__ float load_any(const void *p, int dtype, int64_t i) {
@@ -76,9 +90,16 @@ template <typename T> __device__ __forceinline__ T wave_sum(T v) {
 
 // Sum across groups of `width` consecutive lanes (width a power of two <= 64).
 template <int width> __device__ __forceinline__ float group_sum(float v) {
+  if constexpr (width >= 16) {
+    v = row16_sum(v);
 #pragma unroll
-  for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
-  return v;
+    for (int o = 16; o < width; o <<= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+  } else {
+#pragma unroll
+    for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    return v;
+  }
 }
 
 // MFMA wrappers. Both keep the 16x16 output layout: lane l holds column l%16 and rows

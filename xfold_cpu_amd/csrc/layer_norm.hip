@@ -85,13 +85,21 @@ __global__ __launch_bounds__(256) void ln_rows_vec(const TI *__restrict__ x, int
 #pragma unroll
       for (int i = 0; i < 8; ++i) o[i] = sigmoidf_(sc[i]) * (v[c][i] * rstd) + sh[i];
     } else {
+      float wv[8], bv[8];
+      if (w) {
+        Vec8<float>::load(w + base, wv);
+      } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        float t = v[c][i] * rstd;
-        if (w) t *= w[base + i];
-        if (b) t += b[base + i];
-        o[i] = t;
+        for (int i = 0; i < 8; ++i) wv[i] = 1.f;
       }
+      if (b) {
+        Vec8<float>::load(b + base, bv);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) bv[i] = 0.f;
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = v[c][i] * rstd * wv[i] + bv[i];
     }
     Vec8<TO>::store(yr + base, o);
   }

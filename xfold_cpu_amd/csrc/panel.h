@@ -20,10 +20,35 @@ constexpr int PITCH = K + 8;         // LDS row pitch (bf16) of A and B tiles: 2
 constexpr int A_ELEMS = ROWS * PITCH;
 constexpr int B_ELEMS = CHUNK * PITCH;
 
+// The 8 affine parameters a lane applies (channels sub*8 .. sub*8+7), loaded once.
+struct LnParams {
+  float w[8], b[8];
+};
+
+__device__ __forceinline__ void load_ln_params(const float *w, const float *b, int sub, LnParams &p) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    p.w[i] = 1.f;
+    p.b[i] = 0.f;
+  }
+  if (w) {
+    const float4 lo = reinterpret_cast<const float4 *>(w + sub * 8)[0];
+    const float4 hi = reinterpret_cast<const float4 *>(w + sub * 8)[1];
+    p.w[0] = lo.x; p.w[1] = lo.y; p.w[2] = lo.z; p.w[3] = lo.w;
+    p.w[4] = hi.x; p.w[5] = hi.y; p.w[6] = hi.z; p.w[7] = hi.w;
+  }
+  if (b) {
+    const float4 lo = reinterpret_cast<const float4 *>(b + sub * 8)[0];
+    const float4 hi = reinterpret_cast<const float4 *>(b + sub * 8)[1];
+    p.b[0] = lo.x; p.b[1] = lo.y; p.b[2] = lo.z; p.b[3] = lo.w;
+    p.b[4] = hi.x; p.b[5] = hi.y; p.b[6] = hi.z; p.b[7] = hi.w;
+  }
+}
+
 // LayerNorm of one 128-channel row held by 16 lanes (8 channels each, fp32 statistics),
 // written to the LDS A tile as bf16. `x` holds the lane's 8 inputs.
-__device__ __forceinline__ void ln_row_to_lds(float x[8], const float *w, const float *b, float eps,
-                                              int sub, bf16 *dst_row) {
+__device__ __forceinline__ void ln_row_to_lds(float x[8], const LnParams &p, float eps, int sub,
+                                              bf16 *dst_row) {
   float s = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) s += x[i];
@@ -39,12 +64,7 @@ __device__ __forceinline__ void ln_row_to_lds(float x[8], const float *w, const 
   const float rstd = rsqrtf(q * (1.0f / K) + eps);
   bf16x8 o;
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float t = x[i] * rstd;
-    if (w) t *= w[sub * 8 + i];
-    if (b) t += b[sub * 8 + i];
-    o[i] = bf16(t);
-  }
+  for (int i = 0; i < 8; ++i) o[i] = bf16(x[i] * rstd * p.w[i] + p.b[i]);
   *reinterpret_cast<bf16x8 *>(dst_row + sub * 8) = o;
 }
 
@@ -69,6 +89,8 @@ __device__ __forceinline__ void ln_panel(RowPtr row_ptr, const float *w, const f
                                          bf16 *a_tile) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int sub = lane & 15, rsub = lane >> 4;
+  LnParams prm;
+  load_ln_params(w, b, sub, prm);
   float x[8][8];
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
@@ -84,7 +106,7 @@ __device__ __forceinline__ void ln_panel(RowPtr row_ptr, const float *w, const f
 #pragma unroll
   for (int p = 0; p < 8; ++p) {
     const int r = p * 16 + wave * 4 + rsub;
-    ln_row_to_lds(x[p], w, b, eps, sub, a_tile + r * PITCH);
+    ln_row_to_lds(x[p], prm, eps, sub, a_tile + r * PITCH);
   }
 }
 

@@ -146,12 +146,25 @@ __device__ __forceinline__ void ln_channel_major(const bf16 *x, int64_t plane, i
     }
     __syncthreads();
   }
+  float wk[8], bk[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    wk[i] = 1.f;
+    bk[i] = 0.f;
+  }
+  if (w) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wk[i] = w[kg + 16 * i];
+  }
+  if (b) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) bk[i] = b[kg + 16 * i];
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int k = kg + 16 * i;
-    const float wk = w ? w[k] : 1.f, bk = b ? b[k] : 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a_tile[(pc + e) * PITCH + k] = bf16((v[i][e] - mean[e]) * rstd[e] * wk + bk);
+    for (int e = 0; e < 8; ++e) a_tile[(pc + e) * PITCH + k] = bf16((v[i][e] - mean[e]) * rstd[e] * wk[i] + bk[i]);
   }
 }
 
