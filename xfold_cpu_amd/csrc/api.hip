@@ -114,33 +114,34 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
 // ------------------------------------------------------------------ grid self-attention
 struct GridPlan {
   void *normed, *bias, *qkv, *attn;
-  // fast bf16 path (head dim 32)
-  void *qh, *kh, *vt;
+  // fast bf16 path (c = 128, 4 heads x 32)
+  void *qh, *kh, *vt, *packed;
   float *bias_t;
   uint64_t *maskbits;
 };
 
 static bool grid_fast_path(int64_t c, int64_t heads, int dtype) {
-  return dtype == XFH_BF16 && c / heads == 32 && c % heads == 0;
+  return dtype == XFH_BF16 && c == 128 && heads == 4;
 }
 
 static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t heads, int dtype) {
   const int64_t es = dsize(dtype), plane = n * n;
-  p.normed = cv.take(plane * c * es);
-  p.bias = cv.take(plane * heads * es);
-  p.qkv = cv.take(plane * 3 * c * es);
-  p.attn = cv.take(plane * c * es);
-  p.qh = p.kh = p.vt = nullptr;
-  p.bias_t = nullptr;
-  p.maskbits = nullptr;
+  std::memset(&p, 0, sizeof(p));
   if (grid_fast_path(c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
+    p.packed = cv.take(grid_packed_rows() * c * es);
     p.qh = cv.take(plane * c * es);
     p.kh = cv.take(plane * c * es);
     p.vt = cv.take(n * c * npad * es);
     p.bias_t = static_cast<float *>(cv.take(heads * n * npad * 4));
     p.maskbits = static_cast<uint64_t *>(cv.take(n * (npad / 64) * 8));
+    p.attn = cv.take(plane * c * es);
+    return cv.used;
   }
+  p.normed = cv.take(plane * c * es);
+  p.bias = cv.take(plane * heads * es);
+  p.qkv = cv.take(plane * 3 * c * es);
+  p.attn = cv.take(plane * c * es);
   return cv.used;
 }
 
@@ -388,21 +389,21 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
                                     std::to_string(need) + " bytes)");
   hipStream_t s = as_stream(stream);
   const int64_t plane = n * n, es = dsize(dtype), dh = c / heads;
-  XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, norm_w, norm_b, eps, p.normed, dtype, s));
-  GemmArgs g = gemm_args(p.normed, c, bias_w, c, p.bias, heads, plane, heads, c);
-  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
-  const void *ws[3] = {q_w, k_w, v_w};
-  for (int i = 0; i < 3; ++i) {
-    g = gemm_args(p.normed, c, ws[i], c, static_cast<char *>(p.qkv) + i * c * es, 3 * c, plane, c, c);
-    XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
-  }
   // Batch row b, position t of the (optionally transposed) grid lives at pair row
   // b*n + t (starting node) or t*n + b (ending node); the output keeps pair rows.
   const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
   if (grid_fast_path(c, heads, dtype)) {
-    const float scale = 1.0f / std::sqrt(float(dh));
-    XFH_TRY(grid_attention_prepare(p.qkv, p.bias, mask, mask_dtype, n, int(heads), transpose, scale,
-                                   p.qh, p.kh, p.vt, p.bias_t, p.maskbits, s));
+    const int64_t npad = grid_attention_pad(n);
+    XFH_TRY(grid_pack(q_w, k_w, v_w, bias_w, int(c), int(heads), p.packed, s));
+    GridProjectArgs pa;
+    pa.pair = pair; pa.n = int(n); pa.heads = int(heads); pa.transpose = transpose;
+    pa.ln_w = norm_w; pa.ln_b = norm_b; pa.eps = eps;
+    pa.w_packed = static_cast<const bf16 *>(p.packed);
+    pa.qscale = kLog2e / std::sqrt(float(dh));
+    pa.q = static_cast<bf16 *>(p.qh); pa.k = static_cast<bf16 *>(p.kh); pa.vt = static_cast<bf16 *>(p.vt);
+    pa.bias = p.bias_t; pa.npad = int(npad);
+    XFH_TRY(grid_project(pa, pair_dtype, s));
+    XFH_TRY(grid_mask(mask, mask_dtype, n, npad / 64, p.maskbits, s));
     GridAttentionArgs ga;
     ga.q = static_cast<const bf16 *>(p.qh);
     ga.k = static_cast<const bf16 *>(p.kh);
@@ -413,10 +414,24 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
     ga.osb = row_b * c;
     ga.ost = row_t * c;
     ga.B = int(n); ga.H = int(heads); ga.N = int(n);
-    ga.Npad = int(grid_attention_pad(n));
+    ga.Npad = int(npad);
     ga.Nblk = ga.Npad / 64;
     XFH_TRY(grid_attention(ga, s));
-  } else {
+    GridOutputArgs oa;
+    oa.pair = pair; oa.attn = static_cast<const bf16 *>(p.attn);
+    oa.ln_w = norm_w; oa.ln_b = norm_b; oa.eps = eps;
+    oa.w_gating = static_cast<const bf16 *>(gating_w); oa.w_out = static_cast<const bf16 *>(out_w);
+    oa.out = out; oa.accumulate = accumulate; oa.n = int(n);
+    return grid_output(oa, pair_dtype, out_dtype, s);
+  }
+  XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, norm_w, norm_b, eps, p.normed, dtype, s));
+  GemmArgs g = gemm_args(p.normed, c, bias_w, c, p.bias, heads, plane, heads, c);
+  XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  const void *ws[3] = {q_w, k_w, v_w};
+  for (int i = 0; i < 3; ++i) {
+    g = gemm_args(p.normed, c, ws[i], c, static_cast<char *>(p.qkv) + i * c * es, 3 * c, plane, c, c);
+    XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  }
   AttentionArgs a;
   std::memset(&a, 0, sizeof(a));
   a.q = p.qkv;
@@ -436,7 +451,6 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   a.bs[0] = 0; a.bs[1] = 1; a.bs[2] = n * heads; a.bs[3] = heads;
   a.scale = 1.0f / std::sqrt(float(dh));
   XFH_TRY(attention(a, dtype, s));
-  }
   // attn <- sigmoid(LN(z) Wgate^T) * attn, in place.
   g = gemm_args(p.normed, c, gating_w, c, p.attn, c, plane, c, c);
   g.epi = XFH_EPI_SIGMOID_MUL_AUX; g.aux = p.attn; g.ldaux = c;

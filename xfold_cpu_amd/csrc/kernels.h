@@ -53,6 +53,33 @@ struct GridAttentionArgs {
   int64_t osb, ost;          // out element (b, t, h, d) at out[b*osb + t*ost + h*32 + d]
   int B, H, N, Npad, Nblk;
 };
+// Fused grid-attention projection / output (grid_fused.hip), bf16, c = 128, 4 x 32 heads.
+struct GridProjectArgs {
+  const void *pair;
+  int n, heads, transpose;
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w_packed;      // [3c + 64][c], see grid_pack
+  float qscale;              // d^-0.5 * log2(e)
+  bf16 *q, *k, *vt;
+  float *bias;
+  int npad;
+};
+struct GridOutputArgs {
+  const void *pair;
+  const bf16 *attn;          // [n*n][c], pair-row order
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w_gating, *w_out;
+  void *out;
+  int accumulate, n;
+};
+int64_t grid_packed_rows();
+int grid_pack(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
+              void *packed, hipStream_t s);
+int grid_mask(const void *mask, int mask_dtype, int64_t n, int64_t nblk, uint64_t *bits, hipStream_t s);
+int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s);
+int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 int64_t grid_attention_pad(int64_t n);
 int grid_attention_prepare(const void *qkv, const void *bias_lin, const void *mask, int mask_dtype,
                            int64_t n, int heads, int transpose, float scale, void *qh, void *kh,
