@@ -325,12 +325,12 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
     pa.left = static_cast<bf16 *>(p.left); pa.right = static_cast<bf16 *>(p.right);
     pa.n = int(n); pa.outgoing = outgoing;
     XFH_TRY(trimul_project(pa, pair_dtype, s));
-    GemmArgs g = gemm_args(p.left, n, p.right, n, p.contracted, n, n, n, n);
-    g.sA = plane; g.sB = plane; g.sC = plane;
-    {
-      KernelTimer timer("trimul_contract", s);
-      XFH_TRY(gemm_nt(g, c, dtype, dtype, false, s));
-    }
+    ContractionArgs ca;
+    ca.left = static_cast<const bf16 *>(p.left);
+    ca.right = static_cast<const bf16 *>(p.right);
+    ca.out = static_cast<bf16 *>(p.contracted);
+    ca.n = int(n); ca.channels = int(c);
+    XFH_TRY(contraction(ca, s));
     TriOutputArgs oa;
     oa.pair = pair; oa.contracted = static_cast<const bf16 *>(p.contracted);
     oa.ln_in_w = left_w; oa.ln_in_b = left_b; oa.eps_in = left_eps;

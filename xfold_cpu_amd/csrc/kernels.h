@@ -108,6 +108,12 @@ struct TriOutputArgs {
   void *out;
   int accumulate, n;
 };
+struct ContractionArgs {
+  const bf16 *left, *right;  // [channels][n][n], k-contiguous rows
+  bf16 *out;                 // [channels][n][n]
+  int n, channels;
+};
+int contraction(const ContractionArgs &a, hipStream_t s);
 int trimul_pack(const void *proj, const void *gate, int c, void *packed, hipStream_t s);
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s);
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
