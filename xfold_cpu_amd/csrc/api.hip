@@ -476,6 +476,13 @@ int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t 
               "transition: dtypes must be f32/bf16");
   if (rows == 0) return XFH_OK;
   XFH_REQUIRE(x && out && w1_packed && w2, "transition: null tensor");
+  if (dtype == XFH_BF16 && c == 128 && f == 512) {
+    TransitionArgs ta;
+    ta.x = x; ta.rows = rows; ta.ln_w = norm_w; ta.ln_b = norm_b; ta.eps = eps;
+    ta.w1 = static_cast<const bf16 *>(w1_packed); ta.w2 = static_cast<const bf16 *>(w2);
+    ta.out = out; ta.accumulate = accumulate;
+    return transition_fused(ta, x_dtype, out_dtype, as_stream(stream));
+  }
   Carver cv(workspace, workspace_bytes);
   const int64_t es = dsize(dtype);
   void *normed = cv.take(rows * c * es);

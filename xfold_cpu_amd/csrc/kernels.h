@@ -108,6 +108,19 @@ struct TriOutputArgs {
   void *out;
   int accumulate, n;
 };
+// Fused pair transition (transition_fused.hip), bf16 compute, c = 128, hidden 512.
+struct TransitionArgs {
+  const void *x;
+  int64_t rows;
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w1;            // GLU-packed transition1 weight [1024][128]
+  const bf16 *w2;            // transition2 weight [128][512]
+  void *out;
+  int accumulate;
+};
+int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStream_t s);
+
 struct ContractionArgs {
   const bf16 *left, *right;  // [channels][n][n], k-contiguous rows
   bf16 *out;                 // [channels][n][n]
