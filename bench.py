@@ -38,6 +38,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=3)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--copy-calibration-mb", type=int, default=0,
+                   help="after the run, copy a buffer of this many MiB once (a plain copy kernel of "
+                        "known size whose FETCH_SIZE/WRITE_SIZE counters calibrate the traffic figure)")
     return p.parse_args()
 
 
@@ -205,6 +208,13 @@ def main():
         log("cpu baseline (oracle on host cores)")
         base = cpu_baseline(cfg)
         log(f"cpu baseline: {base}")
+
+    if args.copy_calibration_mb:
+        src = torch.ones(args.copy_calibration_mb << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy calibration: {args.copy_calibration_mb} MiB copied")
 
     dtype = "bf16" if cfg["dtype"] == "bf16" else "fp32"
     line = {
