@@ -280,6 +280,52 @@ def test_grid_self_attention(device, n, transpose, bf16):
                  (pair.to(device), mask.to(device)), bf16, "grid attention", bf16_floor.grid_self_attention)
 
 
+def structured_pair_mask(n, seed):
+    """Mask with every case the bf16 grid-attention kernel distinguishes per key block of 64:
+    fully kept blocks, random holes, a row whose first block is fully masked, a row keeping
+    one key, a column stripe masked for all rows, and fully masked (padding) rows."""
+    g = torch.Generator().manual_seed(seed)
+    mask = (torch.rand(n, n, generator=g) > 0.2).float()
+    mask[8:24] = 1.0                     # row groups whose leading blocks are fully kept
+    mask[3, :64] = 0.0                   # first key block fully masked for row 3
+    mask[5] = 0.0
+    mask[5, n - 12] = 1.0                # a single kept key, in the last (partial) block
+    mask[:, 100:110] = 0.0               # a hole inside the second block, all rows
+    mask[-10:] = 0.0                     # padding rows
+    mask[:, -10:] = 0.0                  # padding keys
+    return mask
+
+
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("sharp", [False, True])
+def test_grid_self_attention_mask_cases(device, transpose, sharp):
+    """bf16 fast path, n = 150 (three key blocks, the last partial). ``sharp`` scales the
+    q/k projections by 2.5 and the bias projection by 4, so that logits span tens of units
+    and the running maximum moves by more than the kernel's rescale slack between blocks;
+    its bf16 rounding is then amplified, so that case is held against the bf16-operand
+    floor (float64 with bf16-rounded matmul operands) rather than the fp32 oracle."""
+    n = 150
+    announce("grid_attention_masks", transpose, sharp)
+    ref, hip = pair_of("GridSelfAttention", dict(c_pair=128, num_head=4, transpose=transpose), seed=7)
+    if sharp:
+        with torch.no_grad():
+            for name, f in (("q_projection", 2.5), ("k_projection", 2.5), ("pair_bias_projection", 4.0)):
+                getattr(ref, name).weight.mul_(f)
+        hip.load_state_dict(ref.state_dict())
+    torch.manual_seed(11)
+    pair = torch.randn(n, n, 128).bfloat16()
+    mask = structured_pair_mask(n, 5)
+    got, want = run_both(ref, hip, (pair.float(), mask), (pair.to(device), mask.to(device)), True)
+    with torch.no_grad():
+        floor = bf16_floor.grid_self_attention(ref.double(), pair.double(), mask.double()).float()
+    ref.float()
+    print(f"[floor] grid masks: oracle vs floor {rel_err(floor, want):.3e}, hip vs oracle "
+          f"{rel_err(got.float().cpu(), want):.3e}, hip vs floor {rel_err(got.float().cpu(), floor):.3e}",
+          flush=True)
+    assert torch.isfinite(got.float()).all()
+    assert_parity_bf16(got, floor if sharp else want, "grid attention mask cases (bf16 store)")
+
+
 @pytest.mark.parametrize("c,f,rows", [(128, 4, (33, 17)), (384, 4, (50,)), (16, 4, (2, 5))])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_transition(device, c, f, rows, bf16):

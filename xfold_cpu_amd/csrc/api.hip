@@ -120,14 +120,14 @@ struct GridPlan {
   uint64_t *maskbits;
 };
 
-static bool grid_fast_path(int64_t c, int64_t heads, int dtype) {
-  return dtype == XFH_BF16 && c == 128 && heads == 4;
+static bool grid_fast_path(int64_t n, int64_t c, int64_t heads, int dtype) {
+  return dtype == XFH_BF16 && c == 128 && heads == 4 && n <= grid_attention_max_n();
 }
 
 static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t heads, int dtype) {
   const int64_t es = dsize(dtype), plane = n * n;
   std::memset(&p, 0, sizeof(p));
-  if (grid_fast_path(c, heads, dtype)) {
+  if (grid_fast_path(n, c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
     p.packed = cv.take(grid_packed_rows() * c * es);
     p.qh = cv.take(plane * c * es);
@@ -392,7 +392,7 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   // Batch row b, position t of the (optionally transposed) grid lives at pair row
   // b*n + t (starting node) or t*n + b (ending node); the output keeps pair rows.
   const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
-  if (grid_fast_path(c, heads, dtype)) {
+  if (grid_fast_path(n, c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
     XFH_TRY(grid_pack(q_w, k_w, v_w, bias_w, int(c), int(heads), p.packed, s));
     GridProjectArgs pa;

@@ -2,7 +2,8 @@
 // c = 128, 4 heads x 32), following GridSelfAttention.forward (xfold/nn/attention.py:80-105):
 //
 //   grid_project: LN(z) -> one GEMM over a packed [q | k | v | bias] weight -> q scaled by
-//       d^-0.5 * log2(e), k, v^T (zero beyond n) and the fp32 pair bias (times log2(e)),
+//       d^-0.5 * log2(e), k, v^T (zero beyond n, keys permuted in runs of 32) and the fp32
+//       pair bias (times log2(e)),
 //       each written straight into the attention kernel's layout (grid_attention.hip).
 //       The bias comes from the un-transposed pair in both directions.
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
@@ -60,15 +61,24 @@ __global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a)
     const int kind = j / 2;                         // 0 q, 1 k, 2 v, 3 bias
     if (kind == 3) {
       // Bias: column h < H of this chunk; bias[h][i][j] for pair (i, j) = (b, t) or (t, b).
+      // The pad columns j in [n, npad) are written as zeros (the attention kernel adds its
+      // mask to them, so they must be finite): by the panels with t >= n when j = t, by the
+      // panels of the last batch row when j = b.
       if (wn == 0 && col < H) {
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             const int t = t0 + wm * 64 + mt * 16 + grp * 4 + e;
-            if (t >= n) continue;
+            if (t >= n) {
+              if (!a.transpose && t < a.npad) a.bias[(int64_t(col) * n + b) * a.npad + t] = 0.0f;
+              continue;
+            }
             const int64_t qi = a.transpose ? t : b, kj = a.transpose ? b : t;
-            a.bias[(int64_t(col) * n + qi) * a.npad + kj] = acc[mt][0][e] * kLog2e;
+            float *row = a.bias + (int64_t(col) * n + qi) * a.npad;
+            row[kj] = acc[mt][0][e] * kLog2e;
+            if (a.transpose && b == n - 1)
+              for (int j = n; j < a.npad; ++j) row[j] = 0.0f;
           }
       }
     } else if (kind < 2) {
@@ -96,6 +106,9 @@ __global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a)
       }
     } else {
       // v: stage transposed [64 cols][128 rows] then [b][h][d][npad] rows, zero beyond n.
+      // Inside every run of 32 keys, position 8g + j holds key 4g + j (j < 4) or
+      // 16 + 4g + (j - 4) (j >= 4): the key order of the attention kernel's P^T fragment,
+      // so that one 16-byte LDS read there yields a whole V^T fragment.
 #pragma unroll
       for (int mt = 0; mt < 4; ++mt)
 #pragma unroll
@@ -109,14 +122,19 @@ __global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int idx = tid + i * 256;              // 64 cols x 16 chunks of 8 rows
-        const int c = idx >> 4, rc = (idx & 15) * 8;
+        const int c = idx >> 4, rc = (idx & 15) * 8;    // positions rc .. rc+7 of the panel
         const int t = t0 + rc;
         if (t >= a.npad) continue;
         const int h = (j & 1) * 2 + c / HD, d = c % HD;
-        bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[c * TPITCH + rc]);
+        const int key0 = (rc & ~31) + ((rc & 31) >> 1);   // panel-relative: 4g, and 16 + 4g
+        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&stage[c * TPITCH + key0]);
+        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&stage[c * TPITCH + key0 + 16]);
+        bf16x8 v;
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (t + e >= n) v[e] = bf16(0.0f);
+        for (int e = 0; e < 4; ++e) {
+          v[e] = t0 + key0 + e < n ? lo[e] : bf16(0.0f);
+          v[4 + e] = t0 + key0 + 16 + e < n ? hi[e] : bf16(0.0f);
+        }
         *reinterpret_cast<bf16x8 *>(a.vt + ((int64_t(b) * H + h) * HD + d) * a.npad + t) = v;
       }
     }

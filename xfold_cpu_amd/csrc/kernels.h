@@ -81,9 +81,7 @@ int grid_mask(const void *mask, int mask_dtype, int64_t n, int64_t nblk, uint64_
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s);
 int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 int64_t grid_attention_pad(int64_t n);
-int grid_attention_prepare(const void *qkv, const void *bias_lin, const void *mask, int mask_dtype,
-                           int64_t n, int heads, int transpose, float scale, void *qh, void *kh,
-                           void *vt, float *bias, uint64_t *maskbits, hipStream_t s);
+int64_t grid_attention_max_n();
 int grid_attention(const GridAttentionArgs &a, hipStream_t s);
 
 // Fused triangle multiplication, bf16 compute, c = 128 (trimul_fused.hip).
