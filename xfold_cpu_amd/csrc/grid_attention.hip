@@ -15,7 +15,7 @@
 //   bias [H][N][Npad] fp32, pre-multiplied by log2(e)
 //   maskbits [B][Npad/64] uint64: bit s%64 of word s/64 set iff key s < N is kept
 //
-// One workgroup = one head, 64 queries (4 wavefronts x 16) and R = 4 batch rows; keys go
+// One workgroup = one head, 128 queries (8 wavefronts x 16) and R = 4 batch rows; keys go
 // in blocks of 64 through a double-buffered LDS stage filled by direct global->LDS loads
 // (one barrier per block). Per block:
 //   - the bias tile [16 q x 64 keys] is loaded once (prefetched a block ahead) and is the
@@ -23,17 +23,20 @@
 //   - the MFMA computes S^T = K Q^T, so a lane holds 16 keys of one query, which is the B
 //     operand of O^T = V^T P^T without any data movement; a constant ones row appended to
 //     V^T makes the same MFMA produce the softmax denominator;
-//   - the row maximum uses v_maximum3 and the gfx950 permlane swaps (no LDS round trip);
 //   - the running maximum is rescaled lazily: o and the denominator are only rescaled
-//     when a block's maximum exceeds the one in use by more than kRescaleSlack (log2
+//     when some key's logit exceeds the maximum in use by more than kRescaleSlack (log2
 //     units), so exp2(s - m) <= 2^kRescaleSlack always, and the final o / l is the same
-//     quotient as with the exact running maximum;
-//   - the Q.K^T of row r+1 is issued before the softmax of row r, so MFMA and VALU work
-//     overlap inside one wavefront;
+//     quotient as with the exact running maximum. The test needs only each lane's own
+//     maximum (v_maximum3); the maximum over a query's four lanes (gfx950 permlane
+//     swaps) is taken only when rescaling;
+//   - the Q.K^T of all rows of the group is issued first, then their softmax and P.V,
+//     giving the scheduler independent MFMA and VALU chains;
 //   - masked keys of a partly kept block get -1e30 added through one more MFMA per key
 //     tile (a rank-1 product), blocks with no kept key are skipped.
 // Workgroups are numbered so that one XCD walks the row groups of one head, keeping that
 // head's bias in its L2.
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -43,21 +46,31 @@ namespace {
 
 constexpr int GD = 32;               // head dim
 constexpr int GKB = 64;              // keys per block
-constexpr int GR = 4;                // batch rows per workgroup
 constexpr int K_ELEMS = GKB * GD;    // K tile of one row: [64 keys][32], 64 B per key
 constexpr int V_ELEMS = GD * GKB;    // V^T tile of one row: [32 d][64 keys], 128 B per d
-constexpr int STAGE_ELEMS = GR * (K_ELEMS + V_ELEMS + GKB);   // + one additive mask row per row
-constexpr int MB_ZERO = 64;
+constexpr int MB_ZERO = 64;          // zeros read by the lanes that supply no mask value
 // Mask words of a row group are kept in LDS: a global read inside the key loop would wait
 // (vmcnt) for the block prefetch issued before it.
-constexpr int kMaxKeyBlocks = 64;     // N <= 4096          // zeros read by the lanes that supply no mask value
+constexpr int kMaxKeyBlocks = 64;    // N <= 4096
 constexpr float kRescaleSlack = 8.0f;
 // Initial running maximum: finite, so that a block whose keys are all masked (logits near
 // kMaskedLogit) neither triggers a rescale nor gets any weight, whatever came before it.
 constexpr float kInitialMax = -1.0e20f;
+constexpr float kMaskedLogit = -1.0e30f;
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
-constexpr float kMaskedLogit = -1.0e30f;
+
+// Workgroup shape: R batch rows, W wavefronts, TQ tiles of 16 queries per wavefront.
+template <int R_, int W_, int TQ_> struct Shape {
+  static constexpr int R = R_, W = W_, TQ = TQ_;
+  static constexpr int Q = 16 * TQ * W;                     // queries per workgroup
+  static constexpr int T = 64 * W;                          // threads
+  static constexpr int STAGE = R * (K_ELEMS + V_ELEMS + GKB); // + one additive mask row per row
+  static constexpr int BLOCKS = 8 / W;                      // workgroups per CU (2 waves per SIMD)
+  static_assert(W >= R, "wavefront r writes row r's mask row");
+  static_assert(8 % W == 0, "each wavefront loads 8 / W of the eight 1 KB pieces of a row");
+};
+using GridShape = Shape<4, 4, 1>;
 
 __device__ __forceinline__ int64_t xcd_logical(int64_t physical, int64_t per_xcd) {
   return (physical % 8) * per_xcd + physical / 8;
@@ -93,20 +106,20 @@ __device__ __forceinline__ float max16(const f32x4 (&s)[4]) {
   return vmax(m, s[3][3]);
 }
 
-__global__ __launch_bounds__(256, 2) void grid_attention_kernel(GridAttentionArgs a) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE_ELEMS + MB_ZERO];
-  auto kbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE_ELEMS + r * K_ELEMS; };
-  auto vbuf = [&](int stage, int r) -> bf16 * {
-    return lds + stage * STAGE_ELEMS + GR * K_ELEMS + r * V_ELEMS;
-  };
+template <class S>
+__global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAttentionArgs a) {
+  constexpr int R = S::R, W = S::W, TQ = S::TQ, GQ = S::Q, GT = S::T, STAGE = S::STAGE;
+  __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE + MB_ZERO];
+  __shared__ uint64_t words[R][kMaxKeyBlocks];       // the group's mask words
+  auto kbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + r * K_ELEMS; };
+  auto vbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + R * K_ELEMS + r * V_ELEMS; };
   auto mbuf = [&](int stage, int r) -> bf16 * {
-    return lds + stage * STAGE_ELEMS + GR * (K_ELEMS + V_ELEMS) + r * GKB;
+    return lds + stage * STAGE + R * (K_ELEMS + V_ELEMS) + r * GKB;
   };
-  bf16 *const mzero = lds + 2 * STAGE_ELEMS;         // MB_ZERO zeros
-  __shared__ uint64_t words[GR][kMaxKeyBlocks];      // the group's mask words
+  bf16 *const mzero = lds + 2 * STAGE;
 
-  const int qblocks = (a.N + 63) / 64;
-  const int rgroups = (a.B + GR - 1) / GR;
+  const int qblocks = (a.N + GQ - 1) / GQ;
+  const int rgroups = (a.B + R - 1) / R;
   const int64_t total = int64_t(qblocks) * rgroups * a.H;
   const int64_t logical = xcd_logical(blockIdx.x, (total + 7) / 8);
   if (logical >= total) return;
@@ -116,37 +129,51 @@ __global__ __launch_bounds__(256, 2) void grid_attention_kernel(GridAttentionArg
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int q = qblk * 64 + wave * 16 + col;
-  const int qc = q < a.N ? q : a.N - 1;
+  // query tile tq of this wavefront: queries q0 + 16 tq + col
+  const int q0 = qblk * GQ + wave * 16 * TQ;
 
-  // Per-row state. A row is active if it exists (b < B) and keeps at least one key.
-  bf16x8 qf[GR];
-  f32x4 o[GR][3];
-  float m[GR];
-  bool all_masked[GR];
-  int active = 0, present = 0;
+  // Per-(row, query tile) state.
+  bf16x8 qf[R][TQ];
+  f32x4 o[R][TQ][3];
+  float m[R][TQ];
 #pragma unroll
-  for (int r = 0; r < GR; ++r) {
-    const int b = rg * GR + r;
-    bf16x8 z = {};
-    qf[r] = z;
-    if (b < a.B && q < a.N)
-      qf[r] = *reinterpret_cast<const bf16x8 *>(a.q + ((int64_t(b) * a.H + h) * a.N + q) * GD + grp * 8);
+  for (int r = 0; r < R; ++r) {
+    const int b = rg * R + r;
 #pragma unroll
-    for (int t = 0; t < 3; ++t) o[r][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m[r] = kInitialMax;
-    uint64_t any = 0;
-    if (b < a.B)
-      for (int w = 0; w < a.Nblk; ++w) any |= a.maskbits[int64_t(b) * a.Nblk + w];
-    all_masked[r] = (b < a.B) && any == 0;
-    if (b < a.B) present |= 1 << r;
-    if (b < a.B && any != 0) active |= 1 << r;
+    for (int tq = 0; tq < TQ; ++tq) {
+      const int q = q0 + 16 * tq + col;
+      bf16x8 z = {};
+      qf[r][tq] = z;
+      if (b < a.B && q < a.N)
+        qf[r][tq] = *reinterpret_cast<const bf16x8 *>(a.q + ((int64_t(b) * a.H + h) * a.N + q) * GD + grp * 8);
+#pragma unroll
+      for (int t = 0; t < 3; ++t) o[r][tq][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m[r][tq] = kInitialMax;
+    }
   }
   if (tid < MB_ZERO) mzero[tid] = bf16(0.0f);
-  for (int i = tid; i < GR * a.Nblk; i += 256) {
-    const int r = i / a.Nblk, w = i % a.Nblk, b = rg * GR + r;
+  for (int i = tid; i < R * a.Nblk; i += GT) {
+    const int r = i / a.Nblk, w = i % a.Nblk, b = rg * R + r;
     words[r][w] = b < a.B ? a.maskbits[int64_t(b) * a.Nblk + w] : 0;
   }
+  __syncthreads();                                   // words, mzero
+  // Row status from the mask words, in every wavefront at once (lane w reads word w):
+  // a row is present if b < B, active if it also keeps some key; first_masked is the
+  // first key block in which some row of the group does not keep all 64 keys.
+  bool all_masked[R];
+  int active = 0, present = 0;
+  uint64_t full_blocks = a.Nblk == 64 ? ~0ull : ((1ull << a.Nblk) - 1);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint64_t w = lane < a.Nblk ? words[r][lane] : 0;
+    const bool any = __ballot(w != 0) != 0;
+    full_blocks &= __ballot(w == ~0ull);
+    const bool here = rg * R + r < a.B;
+    all_masked[r] = here && !any;
+    if (here) present |= 1 << r;
+    if (here && any) active |= 1 << r;
+  }
+  const int first_masked = full_blocks == ~0ull ? a.Nblk : __builtin_ctzll(~full_blocks);
 
   // Swizzled LDS offsets of this lane's K fragment (key kt*16 + col, chunk grp) and V^T
   // fragments (row t*16 + col, chunk 4c + grp); the mask fragment (key kt*16 + col in
@@ -165,96 +192,114 @@ __global__ __launch_bounds__(256, 2) void grid_attention_kernel(GridAttentionArg
 
   // One key block goes global -> LDS without passing through registers
   // (global_load_lds_dwordx4: lane i of a wavefront writes bytes [16i, 16i + 16) of a
-  // 1 KB LDS segment). The 16-byte slots are XOR-swizzled so that the 16 lanes of an
-  // MFMA operand read hit 16 distinct bank groups:
+  // 1 KB LDS segment): per row, four 1 KB pieces of K and four of V^T, spread over the
+  // wavefronts. The 16-byte slots are XOR-swizzled so that the 16 lanes of an MFMA
+  // operand read hit 16 distinct bank groups:
   //   K:   slot s of key j holds its 8-element chunk s ^ ((j >> 2) & 3)
   //   V^T: slot s of row d holds its 8-element chunk s ^ ((d >> 1) & 7)
   // Keys >= N of K are read from key N-1 (their logits are masked); V^T is zero there.
-  // Wavefront r also turns row r's mask word into the additive mask row (0 or -1e30),
-  // before the loads: an LDS store after them would wait for them to land.
+  // From the first block that needs the mask on, wavefront r < R also turns row r's mask
+  // word into the additive mask row (0 or -1e30), before the loads: an LDS store after
+  // them would wait for them to land.
   auto issue = [&](int kb, int stage) {
-    const uint64_t word = words[wave][kb];
-    mbuf(stage, wave)[lane] = ((word >> lane) & 1ull) ? bf16(0.0f) : bf16(kMaskedLogit);
+    if (kb >= first_masked && wave < R) {
+      const uint64_t word = words[wave][kb];
+      mbuf(stage, wave)[lane] = ((word >> lane) & 1ull) ? bf16(0.0f) : bf16(kMaskedLogit);
+    }
 #pragma unroll
-    for (int r = 0; r < GR; ++r) {
-      const int b = rg * GR + r;
-      if (b >= a.B) continue;                          // absent row: its tiles are never read
+    for (int r = 0; r < R; ++r) {
+      const int b = rg * R + r;
+      if (b >= a.B) continue;                        // absent row: its tiles are never read
       const int64_t bh = int64_t(b) * a.H + h;
-      const int key = kb * GKB + wave * 16 + (lane >> 2);
-      const int kchunk = (lane & 3) ^ ((lane >> 4) & 3);
-      const bf16 *ksrc = a.k + (bh * a.N + (key < a.N ? key : a.N - 1)) * GD + kchunk * 8;
-      __builtin_amdgcn_global_load_lds((global_void *)ksrc, (lds_void *)(kbuf(stage, r) + wave * 16 * GD),
-                                       16, 0, 0);
-      const int d = wave * 8 + (lane >> 3);
-      const int vchunk = (lane & 7) ^ ((d >> 1) & 7);
-      const bf16 *vsrc = a.vt + (bh * GD + d) * a.Npad + int64_t(kb) * GKB + vchunk * 8;
-      __builtin_amdgcn_global_load_lds((global_void *)vsrc, (lds_void *)(vbuf(stage, r) + wave * 8 * GKB),
-                                       16, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 8 / W; ++j) {
+        const int piece = wave + j * W;              // 0..3: K keys 16 i.., 4..7: V^T rows 8 i..
+        const int i = piece & 3;
+        if (piece < 4) {
+          const int key = kb * GKB + i * 16 + (lane >> 2);
+          const int kchunk = (lane & 3) ^ ((lane >> 4) & 3);
+          const bf16 *src = a.k + (bh * a.N + (key < a.N ? key : a.N - 1)) * GD + kchunk * 8;
+          __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(kbuf(stage, r) + i * 16 * GD), 16, 0, 0);
+        } else {
+          const int d = i * 8 + (lane >> 3);
+          const int vchunk = (lane & 7) ^ ((d >> 1) & 7);
+          const bf16 *src = a.vt + (bh * GD + d) * a.Npad + int64_t(kb) * GKB + vchunk * 8;
+          __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(vbuf(stage, r) + i * 8 * GKB), 16, 0, 0);
+        }
+      }
     }
   };
   // Waits for this thread's outstanding global loads (LDS transfers included).
   auto drain = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
-  const float *bias_row = a.bias + (int64_t(h) * a.N + qc) * a.Npad;
-  auto load_bias = [&](int kb, f32x4 (&bias)[4]) {
+  // Bias tile of query tile tq: [16 queries x 64 keys], lane (col, grp) holds keys
+  // kt*16 + grp*4 + 0..3 of query q0 + 16 tq + col.
+  const float *bias_rows[TQ];
 #pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-      bias[kt] = *reinterpret_cast<const f32x4 *>(bias_row + kb * GKB + kt * 16 + grp * 4);
-  };
-  // Every row of the group keeps all 64 keys of block kb.
-  auto block_full = [&](int kb) {
-    bool full = true;
+  for (int tq = 0; tq < TQ; ++tq) {
+    const int q = q0 + 16 * tq + col;
+    bias_rows[tq] = a.bias + (int64_t(h) * a.N + (q < a.N ? q : a.N - 1)) * a.Npad;
+  }
+  f32x4 bias[TQ][4];
+  auto load_bias = [&](int kb) {
 #pragma unroll
-    for (int r = 0; r < GR; ++r) full = full && words[r][kb] == ~0ull;
-    return full;
+    for (int tq = 0; tq < TQ; ++tq)
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+        bias[tq][kt] = *reinterpret_cast<const f32x4 *>(bias_rows[tq] + kb * GKB + kt * 16 + grp * 4);
   };
 
-  f32x4 bias[4], bias_next[4];
-
-  // S^T of row r (+ the additive mask row when MASKED) into s.
-  auto scores = [&](int cur, int r, f32x4 (&s)[4], bool masked) {
+  // S^T of row r (+ the additive mask row when masked), both query tiles.
+  auto scores = [&](int cur, int r, f32x4 (&s)[TQ][4], bool masked) {
     const bf16 *kr = kbuf(cur, r);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
       const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kr + (kt * 16 + col) * GD + kslot);
-      s[kt] = mfma16(kf, qf[r], bias[kt]);
+#pragma unroll
+      for (int tq = 0; tq < TQ; ++tq) s[tq][kt] = mfma16(kf, qf[r][tq], bias[tq][kt]);
     }
     if (masked) {
       const bf16 *mr = grp == 0 ? mbuf(cur, r) + col : mzero;
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
         const uint32_t mv = *reinterpret_cast<const uint16_t *>(grp == 0 ? mr + kt * 16 : mr);
-        const uint4 frag = make_uint4(mv, 0u, 0u, 0u);
-        s[kt] = mfma16(__builtin_bit_cast(bf16x8, frag), ones_b, s[kt]);
+        const bf16x8 mf = __builtin_bit_cast(bf16x8, make_uint4(mv, 0u, 0u, 0u));
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) s[tq][kt] = mfma16(mf, ones_b, s[tq][kt]);
       }
     }
   };
-  // P = exp2(S - m) (lazy rescale), then O^T += V^T P^T and l += 1^T P^T.
-  auto softmax_pv = [&](int cur, int r, const f32x4 (&s)[4]) {
-    const float mx = query_max(max16(s));
-    if (__any(mx > m[r] + kRescaleSlack)) {
-      const float mn = vmax(m[r], mx);
-      const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);
+  // Lazy rescale of (row, tile), called when some lane's maximum exceeds m + slack: the
+  // new m is the maximum over the query's four lanes, so it stays the same in all four.
+  auto rescale = [&](int r, int tq, float lane_max) {
+    const float mn = vmax(m[r][tq], query_max(lane_max));
+    const float alpha = __builtin_amdgcn_exp2f(m[r][tq] - mn);
 #pragma unroll
-      for (int t = 0; t < 3; ++t) o[r][t] *= alpha;
-      m[r] = mn;
-    }
-    bf16x8 pf[2];
+    for (int t = 0; t < 3; ++t) o[r][tq][t] *= alpha;
+    m[r][tq] = mn;
+  };
+  // P = exp2(S - m), then O^T += V^T P^T and l += 1^T P^T, both query tiles.
+  auto pv = [&](int cur, int r, const f32x4 (&s)[TQ][4]) {
+    bf16x8 pf[TQ][2];
 #pragma unroll
-    for (int c = 0; c < 2; ++c)
+    for (int tq = 0; tq < TQ; ++tq)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        pf[c][e] = bf16(__builtin_amdgcn_exp2f(s[2 * c][e] - m[r]));
-        pf[c][4 + e] = bf16(__builtin_amdgcn_exp2f(s[2 * c + 1][e] - m[r]));
-      }
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          pf[tq][c][e] = bf16(__builtin_amdgcn_exp2f(s[tq][2 * c][e] - m[r][tq]));
+          pf[tq][c][4 + e] = bf16(__builtin_amdgcn_exp2f(s[tq][2 * c + 1][e] - m[r][tq]));
+        }
     const bf16 *vr = vbuf(cur, r);
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vr + (t * 16 + col) * GKB + vslot[c]);
-        o[r][t] = mfma16(vf, pf[c], o[r][t]);
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) o[r][tq][t] = mfma16(vf, pf[tq][c], o[r][tq][t]);
       }
-      o[r][2] = mfma16(ones_a, pf[c], o[r][2]);
+#pragma unroll
+      for (int tq = 0; tq < TQ; ++tq) o[r][tq][2] = mfma16(ones_a, pf[tq][c], o[r][tq][2]);
     }
   };
   // Row with every key masked: P = 1 on every key of the block. V^T is zero for keys
@@ -269,85 +314,94 @@ __global__ __launch_bounds__(256, 2) void grid_attention_kernel(GridAttentionArg
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vr + (t * 16 + col) * GKB + vslot[c]);
-        o[r][t] = mfma16(vf, ones, o[r][t]);
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) o[r][tq][t] = mfma16(vf, ones, o[r][tq][t]);
       }
   };
-  // All rows active: the Q.K^T of row r+1 is issued before the softmax of row r.
-  auto rows_active = [&](int cur, bool masked) {
-    f32x4 s0[4], s1[4];
-    scores(cur, 0, s0, masked);
+  // One key block for the whole group: the Q.K^T of all (active) rows first, then the next
+  // block's bias into the registers they have just consumed, one rescale test for all
+  // rows, then the exponentials and P.V (independent chains the scheduler interleaves).
+  // MIXED groups (some rows absent or fully masked) test every row's status.
+  auto rows = [&](int cur, int kb, auto masked_c, auto mixed_c) {
+    constexpr bool masked = decltype(masked_c)::value, mixed = decltype(mixed_c)::value;
+    f32x4 s[R][TQ][4];
 #pragma unroll
-    for (int r = 0; r < GR; ++r) {
-      f32x4 (&sc)[4] = (r & 1) ? s1 : s0;
-      f32x4 (&sn)[4] = (r & 1) ? s0 : s1;
-      if (r + 1 < GR) scores(cur, r + 1, sn, masked);
-      softmax_pv(cur, r, sc);
+    for (int r = 0; r < R; ++r)
+      if (!mixed || (active & (1 << r))) scores(cur, r, s[r], masked);
+    if (kb + 1 < a.Nblk) load_bias(kb + 1);
+    float lane_max[R][TQ];
+    bool need = false;
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      if (!mixed || (active & (1 << r)))
+#pragma unroll
+        for (int tq = 0; tq < TQ; ++tq) {
+          lane_max[r][tq] = max16(s[r][tq]);
+          need = need || lane_max[r][tq] > m[r][tq] + kRescaleSlack;
+        }
+    if (__any(need)) {
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        if (!mixed || (active & (1 << r)))
+#pragma unroll
+          for (int tq = 0; tq < TQ; ++tq) rescale(r, tq, lane_max[r][tq]);
     }
-  };
-  // Mixed group (some rows absent or fully masked): row by row.
-  auto rows_mixed = [&](int cur) {
 #pragma unroll
-    for (int r = 0; r < GR; ++r) {
-      if (active & (1 << r)) {
-        f32x4 sr[4];
-        scores(cur, r, sr, true);
-        softmax_pv(cur, r, sr);
-      } else if (present & (1 << r)) {
-        uniform_pv(cur, r);
-      }
+    for (int r = 0; r < R; ++r) {
+      if (!mixed || (active & (1 << r))) pv(cur, r, s[r]);
+      else if (present & (1 << r)) uniform_pv(cur, r);
     }
   };
   // One key block: prefetch the next one into the other stage, compute, hand over.
   auto step = [&](int kb, auto compute) {
     const int cur = kb & 1;
-    const bool more = kb + 1 < a.Nblk;
-    if (more) {
-      issue(kb + 1, cur ^ 1);    // that stage was last read before the previous barrier
-      load_bias(kb + 1, bias_next);
-    }
+    if (kb + 1 < a.Nblk) issue(kb + 1, cur ^ 1);   // that stage was last read before the previous barrier
     compute(cur);
     drain();
     __syncthreads();
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) bias[kt] = bias_next[kt];
   };
 
-  __syncthreads();                                   // words, mzero
   issue(0, 0);
-  load_bias(0, bias);
+  load_bias(0);
   drain();
   __syncthreads();
 
-  const int all_rows = (1 << GR) - 1;
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  const int all_rows = (1 << R) - 1;
   if (active == all_rows) {
     // Leading blocks in which every row keeps every key need no mask; the rest get it.
     int kb = 0;
-    for (; kb < a.Nblk && block_full(kb); ++kb) step(kb, [&](int cur) { rows_active(cur, false); });
-    for (; kb < a.Nblk; ++kb) step(kb, [&](int cur) { rows_active(cur, true); });
+    for (; kb < first_masked; ++kb) step(kb, [&](int cur) { rows(cur, kb, F_{}, F_{}); });
+    for (; kb < a.Nblk; ++kb) step(kb, [&](int cur) { rows(cur, kb, T_{}, F_{}); });
   } else if (active == 0) {
     for (int kb = 0; kb < a.Nblk; ++kb)
       step(kb, [&](int cur) {
 #pragma unroll
-        for (int r = 0; r < GR; ++r)
+        for (int r = 0; r < R; ++r)
           if (present & (1 << r)) uniform_pv(cur, r);
       });
   } else {
-    for (int kb = 0; kb < a.Nblk; ++kb) step(kb, rows_mixed);
+    for (int kb = 0; kb < a.Nblk; ++kb) step(kb, [&](int cur) { rows(cur, kb, T_{}, T_{}); });
   }
 
 #pragma unroll
-  for (int r = 0; r < GR; ++r) {
-    const int b = rg * GR + r;
-    const float l = __shfl(o[r][2][0], col, 64);     // denominator sits in lane `col`, grp 0
-    if (b >= a.B || q >= a.N) continue;
-    const float inv = 1.0f / (all_masked[r] ? float(a.N) : l);
-    bf16 *dst = a.out + int64_t(b) * a.osb + int64_t(q) * a.ost + h * GD + grp * 4;
+  for (int r = 0; r < R; ++r) {
+    const int b = rg * R + r;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      bf16x4 v;
+    for (int tq = 0; tq < TQ; ++tq) {
+      const int q = q0 + 16 * tq + col;
+      const float l = __shfl(o[r][tq][2][0], col, 64);   // denominator sits in lane `col`, grp 0
+      if (b >= a.B || q >= a.N) continue;
+      const float inv = 1.0f / (all_masked[r] ? float(a.N) : l);
+      bf16 *dst = a.out + int64_t(b) * a.osb + int64_t(q) * a.ost + h * GD + grp * 4;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = bf16(o[r][t][e] * inv);
-      *reinterpret_cast<bf16x4 *>(dst + t * 16) = v;
+      for (int t = 0; t < 2; ++t) {
+        bf16x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = bf16(o[r][tq][t][e] * inv);
+        *reinterpret_cast<bf16x4 *>(dst + t * 16) = v;
+      }
     }
   }
 }
@@ -361,12 +415,13 @@ int64_t grid_attention_max_n() { return int64_t(kMaxKeyBlocks) * GKB; }
 int grid_attention(const GridAttentionArgs &a, hipStream_t s) {
   if (a.B == 0 || a.N == 0) return XFH_OK;
   if (a.Nblk > kMaxKeyBlocks) return fail(XFH_EUNSUPPORTED, "grid_attention: more than 4096 keys");
-  const int64_t qblocks = ceil_div(a.N, 64), rgroups = ceil_div(a.B, GR);
+  using S = GridShape;
+  const int64_t qblocks = ceil_div(a.N, S::Q), rgroups = ceil_div(a.B, S::R);
   const int64_t total = qblocks * rgroups * a.H;
   const int64_t grid = ceil_div(total, 8) * 8;
   if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "grid_attention: problem too large");
   KernelTimer timer("grid_attention", s);
-  grid_attention_kernel<<<dim3(grid), 256, 0, s>>>(a);
+  grid_attention_kernel<S><<<dim3(grid), S::T, 0, s>>>(a);
   return check_launch("grid_attention");
 }
 
