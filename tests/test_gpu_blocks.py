@@ -91,7 +91,7 @@ def block_case(n, c_single, mode, pad, seed, device, with_single=True):
 
 
 @pytest.mark.parametrize("n,mode", [(24, "fp32"), (48, "bf16-compute"), (96, "bf16-compute"),
-                                    (48, "bf16"), (96, "bf16")])
+                                    (48, "bf16"), (96, "bf16"), (200, "bf16")])
 def test_pairformer_block(device, n, mode):
     announce("pairformer_block", n, mode)
     (gp, wp), (gs, ws) = block_case(n, 384, mode, pad=3, seed=n, device=device)

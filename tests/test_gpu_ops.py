@@ -245,7 +245,7 @@ def check_module(ref, hip, hip_fn, ref_inputs, dev_inputs, bf16, what, floor_fn=
     return result
 
 
-@pytest.mark.parametrize("n", [5, 37, 64])
+@pytest.mark.parametrize("n", [5, 37, 64, 200])
 @pytest.mark.parametrize("outgoing", [True, False])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_triangle_multiplication(device, n, outgoing, bf16):

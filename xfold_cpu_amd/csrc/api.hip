@@ -95,8 +95,8 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
   std::memset(&p, 0, sizeof(p));
   if (trimul_fast_path(c, dtype)) {
     p.packed = cv.take(4 * c * c * es);
-    p.left = cv.take(plane * c * es);
-    p.right = cv.take(plane * c * es);
+    p.left = cv.take(n * contraction_ld(n) * c * es);
+    p.right = cv.take(n * contraction_ld(n) * c * es);
     p.contracted = cv.take(plane * c * es);
     return cv.used;
   }
@@ -323,13 +323,13 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
     pa.ln_w = left_w; pa.ln_b = left_b; pa.eps = left_eps;
     pa.w_packed = static_cast<const bf16 *>(p.packed);
     pa.left = static_cast<bf16 *>(p.left); pa.right = static_cast<bf16 *>(p.right);
-    pa.n = int(n); pa.outgoing = outgoing;
+    pa.n = int(n); pa.ld = int(contraction_ld(n)); pa.outgoing = outgoing;
     XFH_TRY(trimul_project(pa, pair_dtype, s));
     ContractionArgs ca;
     ca.left = static_cast<const bf16 *>(p.left);
     ca.right = static_cast<const bf16 *>(p.right);
     ca.out = static_cast<bf16 *>(p.contracted);
-    ca.n = int(n); ca.channels = int(c);
+    ca.n = int(n); ca.ld = int(contraction_ld(n)); ca.channels = int(c);
     XFH_TRY(contraction(ca, s));
     TriOutputArgs oa;
     oa.pair = pair; oa.contracted = static_cast<const bf16 *>(p.contracted);

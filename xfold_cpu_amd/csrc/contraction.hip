@@ -3,13 +3,18 @@
 // of xfold/nn/triangle_multiplication.py:96 for both directions (the operand layouts are
 // prepared by trimul_project).
 //
-// Tiling: 128 x 128 output tile per workgroup, k-step 64, 4 wavefronts in a 2 x 2 grid
-// each owning 64 x 64 (4 x 4 MFMA 16x16x32 tiles). Both operand tiles are double-buffered
-// in LDS: the global loads of step s+1 are in flight while step s is multiplied, one
-// barrier per step. The MFMA takes R rows as its A operand so that a lane ends up with
-// four consecutive j of one i and writes them as one 8-byte store. Channels are numbered
-// so that each XCD works through a contiguous run of channels (their operands stay in
-// that XCD's L2).
+// Operands: L, R [channels][n][ld] bf16, ld = contraction_ld(n) (a multiple of 32), with
+// zeros in the columns t in [n, ld) so that the last k-step needs no bounds.
+//
+// Tiling: 192 x 192 output tile per workgroup, 4 wavefronts in a 2 x 2 grid each owning
+// 96 x 96 (6 x 6 MFMA 16x16x32 tiles). Per k-step of 32 both 192 x 32 operand tiles go
+// global -> LDS with global_load_lds_dwordx4 (no registers) into a 3-slot ring, so the
+// loads of step s+2 are in flight while step s is multiplied; one barrier per step. Rows
+// are 64 B in LDS with the 16-byte slots XOR-swizzled (slot c of row r holds chunk
+// c ^ ((r >> 2) & 3)), so the 16 rows of an MFMA operand read hit distinct bank groups.
+// The MFMA takes R rows as its A operand so that a lane ends up with four consecutive j
+// of one i and writes them as one 8-byte store. Channels are numbered so that each XCD
+// works through a contiguous run of tiles (their operands stay in that XCD's L2).
 #include "common.h"
 #include "kernels.h"
 
@@ -17,14 +22,20 @@ namespace xfh {
 
 namespace {
 
-constexpr int TB = 128;                 // tile edge
-constexpr int TK = 64;                  // k-step
-constexpr int TPITCH = TK + 8;          // LDS row pitch (bf16): 144 bytes
-constexpr int TILE_ELEMS = TB * TPITCH;
+constexpr int TB = 192;                 // tile edge
+constexpr int WT = 96;                  // wavefront tile edge
+constexpr int NT = WT / 16;             // MFMA tiles per wavefront edge (6)
+constexpr int TK = 32;                  // k-step
+constexpr int SLOTS = 3;                // ring of operand stages
+constexpr int OP_ELEMS = TB * TK;       // one operand tile (bf16)
+constexpr int SLOT_ELEMS = 2 * OP_ELEMS;
+constexpr int PIECES = 2 * TB / 16;     // 1 KB loads per k-step (24), 6 per wavefront
+typedef __attribute__((address_space(1))) void global_void;
+typedef __attribute__((address_space(3))) void lds_void;
 
 __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) {
-  __shared__ bf16 lds[4 * TILE_ELEMS];   // [stage][L, R] tiles
-  const int n = a.n;
+  __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * SLOT_ELEMS];
+  const int n = a.n, ld = a.ld;
   const int tiles = (n + TB - 1) / TB;
   const int64_t per_channel = int64_t(tiles) * tiles;
   const int64_t total = per_channel * a.channels;
@@ -35,89 +46,77 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
   const int tile = int(logical % per_channel);
   const int i0 = (tile / tiles) * TB, j0 = (tile % tiles) * TB;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wi = wave >> 1, wj = wave & 1, col = lane & 15, grp = lane >> 4;
-  const int64_t plane = int64_t(n) * n;
-  const bf16 *L = a.left + ch * plane;
-  const bf16 *R = a.right + ch * plane;
-  const bool vec = (n % 8) == 0;
+  const int64_t opsize = int64_t(n) * ld;
+  const bf16 *L = a.left + ch * opsize;
+  const bf16 *R = a.right + ch * opsize;
 
-  // 128 rows x 64 k of each operand per stage: 1024 chunks of 16 B -> 4 per thread each.
-  uint4 rl[4], rr[4];
-  auto fetch = [&](int k0) {
+  // Piece p of a k-step: operand p / 12 (L, R), rows 16 (p % 12) .. +15; lane -> row
+  // 16 (p % 12) + lane / 4, LDS slot lane % 4 holding chunk (lane % 4) ^ ((lane >> 4) & 3).
+  // Rows beyond n read row n-1 (their results are never stored).
+  const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
+  const bf16 *src[PIECES / 4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + c * 256;
-      const int r = idx >> 3, kc = (idx & 7) * 8;
-      const int k = k0 + kc;
-      rl[c] = make_uint4(0, 0, 0, 0);
-      rr[c] = make_uint4(0, 0, 0, 0);
-      if (vec) {
-        if (i0 + r < n && k < n) rl[c] = *reinterpret_cast<const uint4 *>(L + int64_t(i0 + r) * n + k);
-        if (j0 + r < n && k < n) rr[c] = *reinterpret_cast<const uint4 *>(R + int64_t(j0 + r) * n + k);
-      } else {
-        bf16 tl[8], tr[8];
+  for (int j = 0; j < PIECES / 4; ++j) {
+    const int p = wave + 4 * j;
+    const int row = (p % 12) * 16 + (lane >> 2);
+    const int g = (p < 12 ? i0 : j0) + row;
+    src[j] = (p < 12 ? L : R) + int64_t(g < n ? g : n - 1) * ld + chunk * 8;
+  }
+  auto issue = [&](int step, int slot) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          tl[e] = (i0 + r < n && k + e < n) ? L[int64_t(i0 + r) * n + k + e] : bf16(0.0f);
-          tr[e] = (j0 + r < n && k + e < n) ? R[int64_t(j0 + r) * n + k + e] : bf16(0.0f);
-        }
-        __builtin_memcpy(&rl[c], tl, 16);
-        __builtin_memcpy(&rr[c], tr, 16);
-      }
-    }
-  };
-  auto stash = [&](int stage) {
-    bf16 *tl = lds + (2 * stage) * TILE_ELEMS, *tr = tl + TILE_ELEMS;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int idx = tid + c * 256;
-      const int r = idx >> 3, kc = (idx & 7) * 8;
-      *reinterpret_cast<uint4 *>(tl + r * TPITCH + kc) = rl[c];
-      *reinterpret_cast<uint4 *>(tr + r * TPITCH + kc) = rr[c];
+    for (int j = 0; j < PIECES / 4; ++j) {
+      const int p = wave + 4 * j;
+      bf16 *dst = lds + slot * SLOT_ELEMS + (p < 12 ? 0 : OP_ELEMS) + (p % 12) * 16 * TK;
+      __builtin_amdgcn_global_load_lds((global_void *)(src[j] + step * TK), (lds_void *)dst, 16, 0, 0);
     }
   };
 
-  f32x4 acc[4][4];   // [jt][it]: rows j (A operand = R), cols i (B operand = L)
-#pragma unroll
-  for (int x = 0; x < 4; ++x)
-#pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+  // Fragment offsets: row r of an operand tile, k-chunk grp, lives at r*TK + slot*8 with
+  // slot = grp ^ ((r >> 2) & 3); for r = base + col with base a multiple of 16 that is
+  // grp ^ ((col >> 2) & 3).
+  const int frag = col * TK + ((grp ^ ((col >> 2) & 3)) * 8);
 
-  const int steps = (n + TK - 1) / TK;
-  fetch(0);
-  stash(0);
-  __syncthreads();
+  f32x4 acc[NT][NT];   // [jt][it]: rows j (A operand = R), cols i (B operand = L)
+#pragma unroll
+  for (int x = 0; x < NT; ++x)
+#pragma unroll
+    for (int y = 0; y < NT; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int steps = ld / TK;
+  issue(0, 0);
+  if (steps > 1) issue(1, 1);
   for (int s = 0; s < steps; ++s) {
-    if (s + 1 < steps) fetch((s + 1) * TK);
-    const bf16 *tl = lds + (2 * (s & 1)) * TILE_ELEMS, *tr = tl + TILE_ELEMS;
-#pragma unroll
-    for (int kk = 0; kk < TK / 32; ++kk) {
-      bf16x8 fr[4], fl[4];
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-        fr[x] = *reinterpret_cast<const bf16x8 *>(tr + (wj * 64 + x * 16 + col) * TPITCH + kk * 32 + grp * 8);
-#pragma unroll
-      for (int y = 0; y < 4; ++y)
-        fl[y] = *reinterpret_cast<const bf16x8 *>(tl + (wi * 64 + y * 16 + col) * TPITCH + kk * 32 + grp * 8);
-#pragma unroll
-      for (int x = 0; x < 4; ++x)
-#pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16(fr[x], fl[y], acc[x][y]);
-    }
-    if (s + 1 < steps) stash((s + 1) & 1);
+    // This wavefront's loads of step s have landed (those of step s+1 may still fly),
+    // then every wavefront's have, and every wavefront is done with step s-1.
+    if (s + 1 < steps) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    if (s + 2 < steps) issue(s + 2, (s + 2) % SLOTS);
+    const bf16 *tl = lds + (s % SLOTS) * SLOT_ELEMS, *tr = tl + OP_ELEMS;
+    bf16x8 fl[NT], fr[NT];
+#pragma unroll
+    for (int y = 0; y < NT; ++y)
+      fl[y] = *reinterpret_cast<const bf16x8 *>(tl + (wi * WT + y * 16) * TK + frag);
+#pragma unroll
+    for (int x = 0; x < NT; ++x) {
+      fr[x] = *reinterpret_cast<const bf16x8 *>(tr + (wj * WT + x * 16) * TK + frag);
+#pragma unroll
+      for (int y = 0; y < NT; ++y) acc[x][y] = mfma16(fr[x], fl[y], acc[x][y]);
+    }
   }
 
-  // acc[x][y][e] = out[i = i0 + wi*64 + y*16 + col][j = j0 + wj*64 + x*16 + grp*4 + e]
-  bf16 *O = a.out + ch * plane;
+  // acc[x][y][e] = out[i = i0 + wi*96 + y*16 + col][j = j0 + wj*96 + x*16 + grp*4 + e]
+  bf16 *O = a.out + ch * int64_t(n) * n;
+  const bool vec = (n % 4) == 0;
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
-    const int i = i0 + wi * 64 + y * 16 + col;
+  for (int y = 0; y < NT; ++y) {
+    const int i = i0 + wi * WT + y * 16 + col;
     if (i >= n) continue;
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      const int j = j0 + wj * 64 + x * 16 + grp * 4;
+    for (int x = 0; x < NT; ++x) {
+      const int j = j0 + wj * WT + x * 16 + grp * 4;
       bf16 *dst = O + int64_t(i) * n + j;
       if (vec && j + 4 <= n) {
         bf16x4 v;
@@ -135,8 +134,11 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
 
 }  // namespace
 
+int64_t contraction_ld(int64_t n) { return align_up(n, TK); }
+
 int contraction(const ContractionArgs &a, hipStream_t s) {
   if (a.n == 0 || a.channels == 0) return XFH_OK;
+  if (a.ld != contraction_ld(a.n)) return fail(XFH_EINVAL, "contraction: operand rows must be padded to 32");
   const int64_t tiles = ceil_div(a.n, TB);
   const int64_t total = tiles * tiles * a.channels;
   const int64_t grid = ceil_div(total, 8) * 8;

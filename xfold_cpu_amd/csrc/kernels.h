@@ -92,8 +92,8 @@ struct TriProjectArgs {
   const float *ln_w, *ln_b;
   float eps;
   const bf16 *w_packed;      // [4c][c], see trimul_pack
-  bf16 *left, *right;        // [c][n][n] contraction operands
-  int n, outgoing;
+  bf16 *left, *right;        // [c][n][ld] contraction operands (contraction_ld), zero-padded
+  int n, ld, outgoing;
 };
 struct TriOutputArgs {
   const void *pair;
@@ -120,10 +120,11 @@ struct TransitionArgs {
 int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStream_t s);
 
 struct ContractionArgs {
-  const bf16 *left, *right;  // [channels][n][n], k-contiguous rows
+  const bf16 *left, *right;  // [channels][n][ld], k-contiguous rows, zero for k >= n
   bf16 *out;                 // [channels][n][n]
-  int n, channels;
+  int n, ld, channels;
 };
+int64_t contraction_ld(int64_t n);
 int contraction(const ContractionArgs &a, hipStream_t s);
 int trimul_pack(const void *proj, const void *gate, int c, void *packed, hipStream_t s);
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s);

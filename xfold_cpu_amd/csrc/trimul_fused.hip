@@ -57,8 +57,7 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
   __syncthreads();
 
   bf16 *left = a.left, *right = a.right;
-  const int64_t plane = int64_t(n) * n;
-  const bool vec = (n % 8) == 0;
+  const int64_t plane = int64_t(n) * a.ld;
   const int chunks = nout / CHUNK;
   for (int j = 0; j < chunks; ++j) {
     if (j + 1 < chunks) fetch_b(a.w_packed, (j + 1) * CHUNK, nout, st);
@@ -75,21 +74,26 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
       *reinterpret_cast<bf16x4 *>(&stage[(wn * 16 + col) * SPITCH + r0]) = v;
     }
     __syncthreads();
-    // 32 projection channels x 128 positions -> left/right[k][x][y0 + ...].
+    // 32 projection channels x 128 positions -> left/right[k][x][y0 + ...], with zeros in
+    // the pad columns y in [n, ld) (ld is a multiple of 32, so a chunk of 8 is either all
+    // below ld or all above).
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int idx = tid + i * 256;
       const int ch = idx >> 4, yc = (idx & 15) * 8;
+      const int y = y0 + yc;
+      if (y >= a.ld) continue;
       const int p = j * 32 + ch;                    // projection channel
       const bool is_a = (p & 1) == 0;
       bf16 *dst = ((a.outgoing != 0) == is_a ? left : right) + int64_t(p >> 1) * plane +
-                  int64_t(x) * n + y0 + yc;
-      const bf16 *src = &stage[ch * SPITCH + yc];
-      if (vec && y0 + yc + 8 <= n) {
-        *reinterpret_cast<bf16x8 *>(dst) = *reinterpret_cast<const bf16x8 *>(src);
-      } else {
-        for (int e = 0; e < 8 && y0 + yc + e < n; ++e) dst[e] = src[e];
+                  int64_t(x) * a.ld + y;
+      bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[ch * SPITCH + yc]);
+      if (y + 8 > n) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (y + e >= n) v[e] = bf16(0.0f);
       }
+      *reinterpret_cast<bf16x8 *>(dst) = v;
     }
     if (j + 1 < chunks) stash_b(st, bbuf(j + 1));
     __syncthreads();
