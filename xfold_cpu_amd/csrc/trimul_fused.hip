@@ -101,18 +101,19 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
 }
 
 // Channel-major LayerNorm of a 128-channel x 128-position tile into the A tile.
-// Thread t holds positions (t%16)*8.. of channels t/16 + 16i (i < 8); sums over the 16
-// channel groups go through two shuffles and a cross-wavefront pass in LDS.
+// Thread t holds channels 8*(t%16) .. +7 of positions 8*(t/16) .. +7, so the 16 lanes of
+// a DPP row hold all 128 channels of the same 8 positions: the statistics need no LDS
+// round trip, and each position's normalised channels leave as 16-byte rows.
 __device__ __forceinline__ void ln_channel_major(const bf16 *x, int64_t plane, int64_t pos0, int valid,
                                                  const float *w, const float *b, float eps,
-                                                 float *red, bf16 *a_tile) {
-  const int tid = threadIdx.x, wave = tid >> 6;
-  const int pc = (tid & 15) * 8, kg = tid >> 4;
+                                                 bf16 *a_tile) {
+  const int tid = threadIdx.x;
+  const int kc = (tid & 15) * 8, pc = (tid >> 4) * 8;
   const bool full = pc + 8 <= valid;
-  float v[8][8];
+  float v[8][8];                                   // [channel kc + i][position pc + e]
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const bf16 *src = x + int64_t(kg + 16 * i) * plane + pos0 + pc;
+    const bf16 *src = x + int64_t(kc + i) * plane + pos0 + pc;
     if (full) {
       load8<bf16>(src, v[i]);
     } else {
@@ -121,54 +122,31 @@ __device__ __forceinline__ void ln_channel_major(const bf16 *x, int64_t plane, i
     }
   }
   float mean[8], rstd[8];
-  // pass 0: mean, pass 1: variance
 #pragma unroll
-  for (int pass = 0; pass < 2; ++pass) {
-    float s[8];
+  for (int e = 0; e < 8; ++e) {
+    float t = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float t = 0.f;
+    for (int i = 0; i < 8; ++i) t += v[i][e];
+    mean[e] = row16_sum(t) * (1.0f / K);
+  }
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float d = pass == 0 ? v[i][e] : v[i][e] - mean[e];
-        t += pass == 0 ? d : d * d;
-      }
-      t += __shfl_xor(t, 16, 64);
-      t += __shfl_xor(t, 32, 64);
-      s[e] = t;
+  for (int e = 0; e < 8; ++e) {
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float d = v[i][e] - mean[e];
+      t += d * d;
     }
-    if ((tid & 63) < 16) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave * ROWS + pc + e] = s[e];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float tot = red[pc + e] + red[ROWS + pc + e] + red[2 * ROWS + pc + e] + red[3 * ROWS + pc + e];
-      if (pass == 0) mean[e] = tot * (1.0f / K);
-      else rstd[e] = rsqrtf(tot * (1.0f / K) + eps);
-    }
-    __syncthreads();
+    rstd[e] = rsqrtf(row16_sum(t) * (1.0f / K) + eps);
   }
-  float wk[8], bk[8];
+  LnParams prm;
+  load_ln_params(w, b, tid & 15, prm);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    wk[i] = 1.f;
-    bk[i] = 0.f;
-  }
-  if (w) {
+  for (int e = 0; e < 8; ++e) {
+    bf16x8 o;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) wk[i] = w[kg + 16 * i];
-  }
-  if (b) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) bk[i] = b[kg + 16 * i];
-  }
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int k = kg + 16 * i;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) a_tile[(pc + e) * PITCH + k] = bf16((v[i][e] - mean[e]) * rstd[e] * wk[i] + bk[i]);
+    for (int i = 0; i < 8; ++i) o[i] = bf16((v[i][e] - mean[e]) * rstd[e] * prm.w[i] + prm.b[i]);
+    *reinterpret_cast<bf16x8 *>(a_tile + (pc + e) * PITCH + kc) = o;
   }
 }
 
@@ -176,7 +154,6 @@ template <typename TIN, typename TOUT>
 __global__ __launch_bounds__(256, 2) void trimul_output_kernel(TriOutputArgs a) {
   __shared__ bf16 lds_a[A_ELEMS];                  // A tile / output staging
   __shared__ bf16 lds_b[2 * B_ELEMS];              // weight chunks
-  __shared__ float red[4 * ROWS];
   auto bbuf = [&](int i) -> bf16 * { return lds_b + (i & 1) * B_ELEMS; };
 
   const int64_t plane = int64_t(a.n) * a.n;
@@ -207,7 +184,7 @@ __global__ __launch_bounds__(256, 2) void trimul_output_kernel(TriOutputArgs a) 
   __syncthreads();                                 // everyone done with lds_a and lds_b
 
   // 2) centre LN of the contraction result -> A fragments; output projection.
-  ln_channel_major(a.contracted, plane, pos0, valid, a.ln_c_w, a.ln_c_b, a.eps_c, red, lds_a);
+  ln_channel_major(a.contracted, plane, pos0, valid, a.ln_c_w, a.ln_c_b, a.eps_c, lds_a);
   fetch_b(a.w_out, 0, K, st);
   stash_b(st, bbuf(0));
   fetch_b(a.w_out, CHUNK, K, st);
