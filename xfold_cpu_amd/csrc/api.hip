@@ -28,6 +28,25 @@ int check_launch(const char *what) {
   return XFH_OK;
 }
 
+int device_cu_count(int *cus) {
+  static std::mutex mu;
+  static std::vector<int> cache;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return fail(XFH_EHIP, std::string("hipGetDevice: ") + hipGetErrorString(err));
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev >= int(cache.size())) cache.resize(dev + 1, 0);
+  if (cache[dev] == 0) {
+    int n = 0;
+    err = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev);
+    if (err != hipSuccess || n <= 0)
+      return fail(XFH_EHIP, std::string("hipDeviceGetAttribute: ") + hipGetErrorString(err));
+    cache[dev] = n;
+  }
+  *cus = cache[dev];
+  return XFH_OK;
+}
+
 // ------------------------------------------------------------------ kernel timing
 namespace {
 struct TimedEvent {

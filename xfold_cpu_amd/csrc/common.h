@@ -48,6 +48,8 @@ class KernelTimer {
   hipStream_t stream_;
   void *start_ = nullptr;
 };
+// Compute units of the current device (cached per device).
+int device_cu_count(int *cus);
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
 

@@ -9,9 +9,12 @@
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
 //       the residual) -> (gate * o) Wout^T -> z += update (or update stored).
 //   grid_mask_words: per batch row, one 64-bit word of kept keys per 64 keys.
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 #include "panel.h"
+#include "rowstep.h"
 
 namespace xfh {
 
@@ -143,109 +146,108 @@ __global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a)
   }
 }
 
+// grid_output, one wavefront per 16 positions at a time (rowstep.h): the gating and
+// output weights stay in LDS for the workgroup's lifetime, the activations never leave
+// the registers, and there is no barrier after the weights are in.
+//   gate^T = Wg . LN(z)^T              (K-layout z -> O-layout gate)
+//   y      = bf16(sigmoid(gate) * o)   (o: attention output rows, K-layout loads moved to
+//                                       O-layout by identity MFMAs)
+//   u^T    = Wout . y^T                (y is the k operand as it stands, Wout in kperm order)
+//   z     += bf16(u)                   (bf16 pair updated in place: the residual is the z
+//                                       already loaded, moved to O-layout the same way)
 template <typename TIN, typename TOUT>
-__global__ __launch_bounds__(256, 2) void grid_output_kernel(GridOutputArgs a) {
-  __shared__ bf16 lds_a[A_ELEMS];
-  __shared__ bf16 lds_b[2 * B_ELEMS];
-  auto bbuf = [&](int i) -> bf16 * { return lds_b + (i & 1) * B_ELEMS; };
+__global__ __launch_bounds__(512, 1) void grid_output_kernel(GridOutputArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 w_gate[rowstep::W_ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 w_out[rowstep::W_ELEMS];
+  __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
+  rowstep::load_weight(a.w_gating, w_gate, false);
+  rowstep::load_weight(a.w_out, w_out, true);
+  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
+  __syncthreads();
 
-  const int64_t plane = int64_t(a.n) * a.n;
-  const int64_t pos0 = int64_t(blockIdx.x) * ROWS;
-  const int valid = int(plane - pos0 < ROWS ? plane - pos0 : ROWS);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
+  const int64_t npos = int64_t(a.n) * a.n;
+  const int64_t steps = (npos + 15) / 16;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int64_t waves = int64_t(gridDim.x) * (blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
-
-  // 1) gate logits from LN(z), in registers.
-  ln_panel<TIN>([&](int r) -> const TIN * { return r < valid ? z + (pos0 + r) * K : nullptr; },
-                a.ln_w, a.ln_b, a.eps, lds_a);
-  __syncthreads();
-  AFrags af;
-  load_a_frags(lds_a, wm, af);
-  BStage st;
-  fetch_b(a.w_gating, 0, K, st);
-  stash_b(st, bbuf(0));
-  fetch_b(a.w_gating, CHUNK, K, st);
-  stash_b(st, bbuf(1));
-  __syncthreads();
-  f32x4 gate[2][4][2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    zero(gate[j]);
-    mma_chunk(af, bbuf(j), wn, gate[j]);
-  }
-  __syncthreads();
-  // 2) A tile <- o (attention output rows), then scaled in place by sigmoid(gate).
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid + i * 256;
-    const int r = idx >> 4, c = (idx & 15) * 8;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (r < valid) v = *reinterpret_cast<const uint4 *>(a.attn + (pos0 + r) * K + c);
-    *reinterpret_cast<uint4 *>(&lds_a[r * PITCH + c]) = v;
-  }
-  fetch_b(a.w_out, 0, K, st);
-  stash_b(st, bbuf(0));
-  fetch_b(a.w_out, CHUNK, K, st);
-  stash_b(st, bbuf(1));
-  __syncthreads();
-#pragma unroll
-  for (int j = 0; j < 2; ++j)
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          bf16 *p = &lds_a[(wm * 64 + mt * 16 + grp * 4 + e) * PITCH + j * CHUNK + wn * 32 + nt * 16 + col];
-          *p = bf16(static_cast<float>(*p) * sigmoidf_(gate[j][mt][nt][e]));
-        }
-  __syncthreads();
-  load_a_frags(lds_a, wm, af);
-  __syncthreads();
-  // 3) output projection -> staging (bf16 update) -> residual.
-  bf16 *stage = lds_a;
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    f32x4 acc[4][2];
-    zero(acc);
-    mma_chunk(af, bbuf(j), wn, acc);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          stage[(wm * 64 + mt * 16 + grp * 4 + e) * PITCH + j * CHUNK + wn * 32 + nt * 16 + col] =
-              bf16(acc[mt][nt][e]);
-  }
-  __syncthreads();
   TOUT *out = static_cast<TOUT *>(a.out);
+  // In-place bf16 update: the residual is the z this kernel reads anyway.
+  constexpr bool kBf16 = sizeof(TIN) == 2 && sizeof(TOUT) == 2;
+  const bool res_from_z = kBf16 && a.accumulate && a.pair == a.out;
+  const bool res_load = a.accumulate && !res_from_z;
+  bf16x8 id[2];
+  rowstep::identity_frags(id);
+
+  struct Rows {
+    rowstep::Raw4<TIN> z[8];                       // K-layout
+    bf16x8 att[4];                                 // K-layout
+    rowstep::Raw4<TOUT> res[8];                    // O-layout (only when not derived from z)
+  };
+  auto fetch = [&](int64_t st, Rows &rw) {
+    const int64_t pos = st * 16 + r, pc = pos < npos ? pos : npos - 1;
+    rowstep::load_k<TIN>(z + pc * K, rw.z);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid + i * 256;
-    const int r = idx >> 4, c = (idx & 15) * 8;
-    if (r >= valid) continue;
-    TOUT *dst = out + (pos0 + r) * K + c;
-    float u[8], o[8];
-    load8<bf16>(&stage[r * PITCH + c], u);
-    if (a.accumulate) {
-      load8<TOUT>(dst, o);
+    for (int ks = 0; ks < 4; ++ks) rw.att[ks] = *reinterpret_cast<const bf16x8 *>(a.attn + pc * K + 32 * ks + 8 * g);
+    if (res_load) rowstep::load_o<TOUT>(out + pc * K, rw.res);
+  };
+  // Rows of the next step are loaded while this one is computed.
+  int64_t st = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  Rows cur;
+  if (st < steps) fetch(st, cur);
+  for (; st < steps; st += waves) {
+    Rows next;
+    if (st + waves < steps) fetch(st + waves, next);
+    bf16x8 x[4];
+    {
+      float v[32];
+      rowstep::k_to_float(cur.z, v);
+      rowstep::ln_k(v, lnw, lnb, a.eps, x);
+    }
+    f32x4 acc[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += u[e];
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rowstep::gemm_t(w_gate, x, acc);
+    f32x4 att[8];
+    rowstep::k_to_o(id, cur.att, att);
+    float y[8][4];
+#pragma unroll
+    for (int t = 0; t < 8; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[t][e] = sigmoidf_(acc[t][e]) * att[t][e];
+    rowstep::o_to_operand(y, x);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rowstep::gemm_t(w_out, x, acc);
+    f32x4 res[8];
+    if (res_from_z) {
+      if constexpr (kBf16) {
+        bf16x8 zk[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            zk[ks][e] = cur.z[2 * ks].v[e];
+            zk[ks][4 + e] = cur.z[2 * ks + 1].v[e];
+          }
+        rowstep::k_to_o(id, zk, res);
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = u[e];
-    }
-    if constexpr (sizeof(TOUT) == 2) {
-      bf16x8 w;
+      for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = bf16(o[e]);
-      *reinterpret_cast<bf16x8 *>(dst) = w;
-    } else {
-      reinterpret_cast<float4 *>(dst)[0] = make_float4(o[0], o[1], o[2], o[3]);
-      reinterpret_cast<float4 *>(dst)[1] = make_float4(o[4], o[5], o[6], o[7]);
+        for (int e = 0; e < 4; ++e) res[t][e] = res_load ? cur.res[t][e] : 0.f;
     }
+    const int64_t pos = st * 16 + r;
+    if (pos < npos) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = res[t][e] + static_cast<float>(bf16(acc[t][e]));  // bf16 update
+        rowstep::store4f<TOUT>(out + pos * K + 16 * t + 4 * g, o);
+      }
+    }
+    cur = next;
   }
 }
 
@@ -307,16 +309,19 @@ int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {
 }
 
 int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s) {
-  const int64_t panels = ceil_div(int64_t(a.n) * a.n, ROWS);
+  const int64_t steps = ceil_div(int64_t(a.n) * a.n, 16);
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(steps, 8))));
   KernelTimer timer("grid_output", s);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    grid_output_kernel<bf16, bf16><<<dim3(panels), 256, 0, s>>>(a);
+    grid_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
   else if (pair_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    grid_output_kernel<bf16, float><<<dim3(panels), 256, 0, s>>>(a);
+    grid_output_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
   else if (pair_dtype == XFH_F32 && out_dtype == XFH_F32)
-    grid_output_kernel<float, float><<<dim3(panels), 256, 0, s>>>(a);
+    grid_output_kernel<float, float><<<grid, 512, 0, s>>>(a);
   else
-    grid_output_kernel<float, bf16><<<dim3(panels), 256, 0, s>>>(a);
+    grid_output_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
   return check_launch("grid_output");
 }
 

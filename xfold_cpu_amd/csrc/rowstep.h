@@ -1,0 +1,228 @@
+// Register-resident building blocks for the pair-stack kernels whose inputs and outputs
+// are [positions][128 channels] rows (bf16 compute, K = 128).
+//
+// A wavefront works on 16 positions at a time ("step") with no LDS traffic for its
+// activations and no barriers: lane l handles position l % 16 and channel group
+// g = l / 16, and the activations live in one of two register layouts:
+//   K-layout: channels 32 ks + 8 g + j (ks < 4, j < 8), the MFMA operand layout with
+//             k = channels (a lane supplies 8 consecutive k per 16x16x32 step);
+//   O-layout: channels 16 t + 4 g + e (t < 8, e < 4), the layout of a 16x16 MFMA result
+//             tile whose columns are positions and whose rows are channels.
+// An O-layout set is also a valid MFMA k-operand if the other operand lists its k in the
+// order kperm(ks, g, j) below (tiles 2 ks and 2 ks + 1 side by side), so a result feeds
+// the next GEMM without leaving the registers.
+//
+// Weights W[128 out][128 in] (nn.Linear layout) sit in LDS for the workgroup's lifetime,
+// 256-byte rows with 16-byte chunk c of row n stored at chunk c ^ (n & 15), optionally with
+// their input channels in kperm order. out^T[n][pos] = sum_k W[n][k] x[pos][k] then takes
+// W as the A operand (row n = 16 t + l % 16) and x as the B operand, and lands in O-layout.
+#pragma once
+
+#include "common.h"
+
+namespace xfh {
+namespace rowstep {
+
+constexpr int C = 128;                  // channels
+constexpr int W_ELEMS = C * C;          // one weight matrix in LDS (bf16, 32 KB)
+
+// Input channel of MFMA k-slot (ks, g, j) when the operand is an O-layout register set.
+__host__ __device__ constexpr int kperm(int ks, int g, int j) {
+  return j < 4 ? 32 * ks + 4 * g + j : 32 * ks + 16 + 4 * g + (j - 4);
+}
+
+// Copies W ([128][128] bf16, row-major) into LDS with the chunk swizzle; `permuted`
+// reorders each row's input channels to kperm order. All threads of the workgroup take part.
+__device__ __forceinline__ void load_weight(const bf16 *__restrict__ w, bf16 *dst, bool permuted) {
+  for (int i = threadIdx.x; i < C * 16; i += blockDim.x) {
+    const int n = i >> 4, c = i & 15;              // destination row, logical chunk
+    const int ks = c >> 2, g = c & 3;
+    bf16x8 v;
+    if (permuted) {
+      const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(w + n * C + kperm(ks, g, 0));
+      const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(w + n * C + kperm(ks, g, 4));
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = lo[e];
+        v[4 + e] = hi[e];
+      }
+    } else {
+      v = *reinterpret_cast<const bf16x8 *>(w + n * C + c * 8);
+    }
+    *reinterpret_cast<bf16x8 *>(dst + n * C + ((c ^ (n & 15)) * 8)) = v;
+  }
+}
+
+// A fragment of W for output tile t, k-step ks (lane: row 16 t + l % 16, chunk 4 ks + g).
+__device__ __forceinline__ bf16x8 weight_frag(const bf16 *w_lds, int t, int ks) {
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int n = 16 * t + r;
+  return *reinterpret_cast<const bf16x8 *>(w_lds + n * C + (((4 * ks + g) ^ r) * 8));
+}
+
+// out^T tiles: acc[t] (+)= sum_ks W(t, ks) . x[ks]; x is a K-layout (or, with a permuted W,
+// an O-layout) bf16 operand.
+__device__ __forceinline__ void gemm_t(const bf16 *w_lds, const bf16x8 (&x)[4], f32x4 (&acc)[8]) {
+#pragma unroll
+  for (int t = 0; t < 8; ++t)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc[t] = mfma16(weight_frag(w_lds, t, ks), x[ks], acc[t]);
+}
+
+// Sum over the four lanes of one position (l, l ^ 16, l ^ 32, l ^ 48). The swap results
+// pass through an empty asm: the compiler otherwise folds arithmetic on the two results
+// of one swap as if they were equal.
+__device__ __forceinline__ float position_sum(float x) {
+  uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto p = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  uint32_t p0 = p[0], p1 = p[1];
+  asm volatile("" : "+v"(p0), "+v"(p1));
+  x = __builtin_bit_cast(float, p0) + __builtin_bit_cast(float, p1);
+  u = __builtin_bit_cast(uint32_t, x);
+  const auto q = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  uint32_t q0 = q[0], q1 = q[1];
+  asm volatile("" : "+v"(q0), "+v"(q1));
+  return __builtin_bit_cast(float, q0) + __builtin_bit_cast(float, q1);
+}
+
+// LayerNorm statistics of a position from this lane's 32 channels (fp32, two passes).
+__device__ __forceinline__ void ln_stats(const float (&v)[32], float eps, float &mean, float &rstd) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s += v[i];
+  mean = position_sum(s) * (1.0f / C);
+  float q = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float d = v[i] - mean;
+    q += d * d;
+  }
+  rstd = rsqrtf(position_sum(q) * (1.0f / C) + eps);
+}
+
+// Loads 8 consecutive channels of a row as floats.
+template <typename T> __device__ __forceinline__ void load8f(const T *p, float *o);
+template <> __device__ __forceinline__ void load8f<bf16>(const bf16 *p, float *o) {
+  const bf16x8 v = *reinterpret_cast<const bf16x8 *>(p);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) o[i] = static_cast<float>(v[i]);
+}
+template <> __device__ __forceinline__ void load8f<float>(const float *p, float *o) {
+  const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+  o[4] = b.x; o[5] = b.y; o[6] = b.z; o[7] = b.w;
+}
+template <typename T> __device__ __forceinline__ void load4f(const T *p, float *o);
+template <> __device__ __forceinline__ void load4f<bf16>(const bf16 *p, float *o) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4 *>(p);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = static_cast<float>(v[i]);
+}
+template <> __device__ __forceinline__ void load4f<float>(const float *p, float *o) {
+  const float4 a = *reinterpret_cast<const float4 *>(p);
+  o[0] = a.x; o[1] = a.y; o[2] = a.z; o[3] = a.w;
+}
+template <typename T> __device__ __forceinline__ void store4f(T *p, const float *v);
+template <> __device__ __forceinline__ void store4f<bf16>(bf16 *p, const float *v) {
+  bf16x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = bf16(v[i]);
+  *reinterpret_cast<bf16x4 *>(p) = o;
+}
+template <> __device__ __forceinline__ void store4f<float>(float *p, const float *v) {
+  *reinterpret_cast<float4 *>(p) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+// Four consecutive channels as loaded (bf16x4 or float4), converted only when used, so
+// that loads can be issued early without holding fp32 copies.
+template <typename T> struct Raw4;
+template <> struct Raw4<bf16> {
+  bf16x4 v;
+  __device__ __forceinline__ void load(const bf16 *p) { v = *reinterpret_cast<const bf16x4 *>(p); }
+  __device__ __forceinline__ float operator[](int i) const { return static_cast<float>(v[i]); }
+};
+template <> struct Raw4<float> {
+  float4 v;
+  __device__ __forceinline__ void load(const float *p) { v = *reinterpret_cast<const float4 *>(p); }
+  __device__ __forceinline__ float operator[](int i) const { return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w; }
+};
+
+// K-layout row as loaded: r[2 ks + h] = channels 32 ks + 8 g + 4 h .. +3.
+template <typename T> __device__ __forceinline__ void load_k(const T *row, Raw4<T> (&r)[8]) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    r[2 * ks].load(row + 32 * ks + 8 * g);
+    r[2 * ks + 1].load(row + 32 * ks + 8 * g + 4);
+  }
+}
+template <typename T> __device__ __forceinline__ void k_to_float(const Raw4<T> (&r)[8], float (&v)[32]) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[4 * i + e] = r[i][e];
+}
+// O-layout row as loaded: r[t] = channels 16 t + 4 g .. +3.
+template <typename T> __device__ __forceinline__ void load_o(const T *row, Raw4<T> (&r)[8]) {
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) r[t].load(row + 16 * t + 4 * g);
+}
+
+// LayerNorm of a K-layout position (affine parameters from LDS, fp32) to bf16 operands.
+__device__ __forceinline__ void ln_k(float (&v)[32], const float *lnw, const float *lnb, float eps,
+                                     bf16x8 (&x)[4]) {
+  const int g = (threadIdx.x & 63) >> 4;
+  float mean, rstd;
+  ln_stats(v, eps, mean, rstd);
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const float4 w0 = *reinterpret_cast<const float4 *>(lnw + 32 * ks + 8 * g);
+    const float4 w1 = *reinterpret_cast<const float4 *>(lnw + 32 * ks + 8 * g + 4);
+    const float4 b0 = *reinterpret_cast<const float4 *>(lnb + 32 * ks + 8 * g);
+    const float4 b1 = *reinterpret_cast<const float4 *>(lnb + 32 * ks + 8 * g + 4);
+    const float wv[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    const float bv[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[ks][j] = bf16((v[8 * ks + j] - mean) * rstd * wv[j] + bv[j]);
+  }
+}
+
+// Copies optional LayerNorm affine parameters (fp32[128], nullptr: 1 / 0) into LDS.
+__device__ __forceinline__ void load_ln(const float *w, const float *b, float *w_lds, float *b_lds) {
+  for (int i = threadIdx.x; i < C; i += blockDim.x) {
+    w_lds[i] = w ? w[i] : 1.f;
+    b_lds[i] = b ? b[i] : 0.f;
+  }
+}
+
+// Identity fragments: as the A operand with a K-layout operand x[ks] as B, half h
+// (0 or 1) gives O-layout tile t = 2 ks + h exactly (one nonzero product per output), so
+// one MFMA both converts 16 bf16 channels per position to fp32 and moves them into O-layout.
+__device__ __forceinline__ void identity_frags(bf16x8 (&id)[2]) {
+  const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) id[h][j] = (8 * g + j == m + 16 * h) ? bf16(1.0f) : bf16(0.0f);
+}
+__device__ __forceinline__ void k_to_o(const bf16x8 (&id)[2], const bf16x8 (&x)[4], f32x4 (&o)[8]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) o[2 * ks + h] = mfma16(id[h], x[ks], f32x4{0.f, 0.f, 0.f, 0.f});
+}
+
+// Pairs the O-layout values of tiles 2 ks and 2 ks + 1 into k-operand ks (kperm order).
+__device__ __forceinline__ void o_to_operand(const float (&y)[8][4], bf16x8 (&x)[4]) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      x[ks][e] = bf16(y[2 * ks][e]);
+      x[ks][4 + e] = bf16(y[2 * ks + 1][e]);
+    }
+}
+
+}  // namespace rowstep
+}  // namespace xfh
