@@ -8,10 +8,14 @@
 //       times sigmoid(gating_linear(LN_in(z))) (recomputed from z, which this kernel reads
 //       anyway for the residual) -> z += update (or update stored).
 //
-// Both are row-panel kernels (panel.h): 128 pair positions per workgroup.
+// trimul_project is a row-panel kernel (panel.h, 128 pair positions per workgroup);
+// trimul_output works on register-resident rows (rowstep.h).
+#include <algorithm>
+
 #include "common.h"
 #include "kernels.h"
 #include "panel.h"
+#include "rowstep.h"
 
 namespace xfh {
 
@@ -100,145 +104,149 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
   }
 }
 
-// Channel-major LayerNorm of a 128-channel x 128-position tile into the A tile.
-// Thread t holds channels 8*(t%16) .. +7 of positions 8*(t/16) .. +7, so the 16 lanes of
-// a DPP row hold all 128 channels of the same 8 positions: the statistics need no LDS
-// round trip, and each position's normalised channels leave as 16-byte rows.
-__device__ __forceinline__ void ln_channel_major(const bf16 *x, int64_t plane, int64_t pos0, int valid,
-                                                 const float *w, const float *b, float eps,
-                                                 bf16 *a_tile) {
-  const int tid = threadIdx.x;
-  const int kc = (tid & 15) * 8, pc = (tid >> 4) * 8;
-  const bool full = pc + 8 <= valid;
-  float v[8][8];                                   // [channel kc + i][position pc + e]
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const bf16 *src = x + int64_t(kc + i) * plane + pos0 + pc;
-    if (full) {
-      load8<bf16>(src, v[i]);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[i][e] = (pc + e < valid) ? static_cast<float>(src[e]) : 0.f;
-    }
-  }
-  float mean[8], rstd[8];
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) t += v[i][e];
-    mean[e] = row16_sum(t) * (1.0f / K);
-  }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    float t = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float d = v[i][e] - mean[e];
-      t += d * d;
-    }
-    rstd[e] = rsqrtf(row16_sum(t) * (1.0f / K) + eps);
-  }
-  LnParams prm;
-  load_ln_params(w, b, tid & 15, prm);
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    bf16x8 o;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = bf16((v[i][e] - mean[e]) * rstd[e] * prm.w[i] + prm.b[i]);
-    *reinterpret_cast<bf16x8 *>(a_tile + (pc + e) * PITCH + kc) = o;
-  }
-}
-
+// trimul_output, one wavefront per 16 positions at a time (rowstep.h), weights resident in
+// LDS, activations in registers, no barriers after the weights are in:
+//   gate^T = Wg . LN_in(z)^T                  (K-layout z -> O-layout gate logits)
+//   c      = contraction result, channel-major: 16-byte loads of 8 positions of a channel
+//            are an MFMA A fragment, times an identity B (either k-half) they land in
+//            O-layout (exact)
+//   y      = bf16(LN_c(c))                    (statistics over the 4 lanes of a position)
+//   u^T    = Wout . y^T                       (Wout in kperm order)
+//   z     += bf16(u * sigmoid(gate))
 template <typename TIN, typename TOUT>
-__global__ __launch_bounds__(256, 2) void trimul_output_kernel(TriOutputArgs a) {
-  __shared__ bf16 lds_a[A_ELEMS];                  // A tile / output staging
-  __shared__ bf16 lds_b[2 * B_ELEMS];              // weight chunks
-  auto bbuf = [&](int i) -> bf16 * { return lds_b + (i & 1) * B_ELEMS; };
+__global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 w_gate[rowstep::W_ELEMS];
+  __shared__ __attribute__((aligned(16))) bf16 w_out[rowstep::W_ELEMS];
+  __shared__ __attribute__((aligned(16))) float lnw_in[K], lnb_in[K], lnw_c[K], lnb_c[K];
+  rowstep::load_weight(a.w_gating, w_gate, false);
+  rowstep::load_weight(a.w_out, w_out, true);
+  rowstep::load_ln(a.ln_in_w, a.ln_in_b, lnw_in, lnb_in);
+  rowstep::load_ln(a.ln_c_w, a.ln_c_b, lnw_c, lnb_c);
+  __syncthreads();
 
-  const int64_t plane = int64_t(a.n) * a.n;
-  const int64_t pos0 = int64_t(blockIdx.x) * ROWS;
-  const int valid = int(plane - pos0 < ROWS ? plane - pos0 : ROWS);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
+  const int64_t npos = int64_t(a.n) * a.n;
+  const int64_t steps = (npos + 15) / 16;
+  const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
+  const int64_t waves = int64_t(gridDim.x) * (blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
-
-  // 1) gate = sigmoid(LN_in(z) Wgating^T), kept in registers for this wavefront's block.
-  ln_panel<TIN>([&](int r) -> const TIN * { return r < valid ? z + (pos0 + r) * K : nullptr; },
-                a.ln_in_w, a.ln_in_b, a.eps_in, lds_a);
-  __syncthreads();
-  AFrags af;
-  load_a_frags(lds_a, wm, af);
-  BStage st;
-  fetch_b(a.w_gating, 0, K, st);
-  stash_b(st, bbuf(0));
-  fetch_b(a.w_gating, CHUNK, K, st);
-  stash_b(st, bbuf(1));
-  __syncthreads();
-  f32x4 gate[2][4][2];
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    zero(gate[j]);
-    mma_chunk(af, bbuf(j), wn, gate[j]);
-  }
-  __syncthreads();                                 // everyone done with lds_a and lds_b
-
-  // 2) centre LN of the contraction result -> A fragments; output projection.
-  ln_channel_major(a.contracted, plane, pos0, valid, a.ln_c_w, a.ln_c_b, a.eps_c, lds_a);
-  fetch_b(a.w_out, 0, K, st);
-  stash_b(st, bbuf(0));
-  fetch_b(a.w_out, CHUNK, K, st);
-  stash_b(st, bbuf(1));
-  __syncthreads();
-  load_a_frags(lds_a, wm, af);
-  __syncthreads();                                 // A tile free for output staging
-  bf16 *stage = lds_a;                             // [128 positions][PITCH]
-#pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    f32x4 acc[4][2];
-    zero(acc);
-    mma_chunk(af, bbuf(j), wn, acc);
-#pragma unroll
-    for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-      for (int nt = 0; nt < 2; ++nt) {
-        const int c = j * CHUNK + wn * 32 + nt * 16 + col;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = wm * 64 + mt * 16 + grp * 4 + e;
-          stage[r * PITCH + c] = bf16(acc[mt][nt][e] * sigmoidf_(gate[j][mt][nt][e]));
-        }
-      }
-  }
-  __syncthreads();
-  // 3) residual: 128 positions x 128 channels, 8 channels per thread-chunk.
   TOUT *out = static_cast<TOUT *>(a.out);
+  constexpr bool kBf16 = sizeof(TIN) == 2 && sizeof(TOUT) == 2;
+  const bool res_from_z = kBf16 && a.accumulate && a.pair == a.out;
+  const bool res_load = a.accumulate && !res_from_z;
+  const bool c_vec = (npos % 8) == 0;
+  bf16x8 id[2];
+  rowstep::identity_frags(id);
+
+  struct Rows {
+    rowstep::Raw4<TIN> z[8];                       // K-layout
+    bf16x8 c[4];                                   // see fetch
+    rowstep::Raw4<TOUT> res[8];                    // O-layout (only when not derived from z)
+  };
+  auto fetch = [&](int64_t st, Rows &rw) {
+    const int64_t pos = st * 16 + r, pc = pos < npos ? pos : npos - 1;
+    rowstep::load_k<TIN>(z + pc * K, rw.z);
+    // c[q]: channel 16 q + r (g < 2) or 16 (q + 4) + r (g >= 2), positions 8 (g % 2) .. +7
+    // of the step: k = 8 g + j of an A fragment whose k-halves hold tiles q and q + 4.
+    const int64_t p0 = st * 16 + 8 * (g & 1);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int idx = tid + i * 256;
-    const int r = idx >> 4, c = (idx & 15) * 8;
-    if (r >= valid) continue;
-    TOUT *dst = out + (pos0 + r) * K + c;
-    float u[8];
-    load8<bf16>(&stage[r * PITCH + c], u);
-    float o[8];
-    if (a.accumulate) {
-      load8<TOUT>(dst, o);
+    for (int q = 0; q < 4; ++q) {
+      const bf16 *src = a.contracted + int64_t(16 * (q + 4 * (g >> 1)) + r) * npos + p0;
+      bf16x8 v = {};
+      if (c_vec && p0 + 8 <= npos) {
+        v = *reinterpret_cast<const bf16x8 *>(src);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] += u[e];
+        for (int j = 0; j < 8; ++j)
+          if (p0 + j < npos) v[j] = src[j];
+      }
+      rw.c[q] = v;
+    }
+    if (res_load) rowstep::load_o<TOUT>(out + pc * K, rw.res);
+  };
+
+  int64_t st = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  Rows cur;
+  if (st < steps) fetch(st, cur);
+  for (; st < steps; st += waves) {
+    Rows next;
+    if (st + waves < steps) fetch(st + waves, next);
+    // gate = sigmoid(Wg . LN_in(z))
+    float sig[8][4];
+    {
+      bf16x8 x[4];
+      float v[32];
+      rowstep::k_to_float(cur.z, v);
+      rowstep::ln_k(v, lnw_in, lnb_in, a.eps_in, x);
+      f32x4 acc[8];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      rowstep::gemm_t(w_gate, x, acc);
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) sig[t][e] = sigmoidf_(acc[t][e]);
+    }
+    // y = LN_c(c), O-layout
+    bf16x8 y[4];
+    {
+      f32x4 co[8];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        co[q] = mfma16(cur.c[q], id[0], f32x4{0.f, 0.f, 0.f, 0.f});
+        co[q + 4] = mfma16(cur.c[q], id[1], f32x4{0.f, 0.f, 0.f, 0.f});
+      }
+      float v[32];
+#pragma unroll
+      for (int t = 0; t < 8; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[4 * t + e] = co[t][e];
+      float mean, rstd;
+      rowstep::ln_stats(v, a.eps_c, mean, rstd);
+      float yo[8][4];
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const float4 w = *reinterpret_cast<const float4 *>(lnw_c + 16 * t + 4 * g);
+        const float4 b = *reinterpret_cast<const float4 *>(lnb_c + 16 * t + 4 * g);
+        const float wv[4] = {w.x, w.y, w.z, w.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) yo[t][e] = (v[4 * t + e] - mean) * rstd * wv[e] + bv[e];
+      }
+      rowstep::o_to_operand(yo, y);
+    }
+    f32x4 acc[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
+    rowstep::gemm_t(w_out, y, acc);
+    f32x4 res[8];
+    if (res_from_z) {
+      if constexpr (kBf16) {
+        bf16x8 zk[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            zk[ks][e] = cur.z[2 * ks].v[e];
+            zk[ks][4 + e] = cur.z[2 * ks + 1].v[e];
+          }
+        rowstep::k_to_o(id, zk, res);
+      }
     } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = u[e];
-    }
-    if constexpr (sizeof(TOUT) == 2) {
-      bf16x8 w;
+      for (int t = 0; t < 8; ++t)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) w[e] = bf16(o[e]);
-      *reinterpret_cast<bf16x8 *>(dst) = w;
-    } else {
-      reinterpret_cast<float4 *>(dst)[0] = make_float4(o[0], o[1], o[2], o[3]);
-      reinterpret_cast<float4 *>(dst)[1] = make_float4(o[4], o[5], o[6], o[7]);
+        for (int e = 0; e < 4; ++e) res[t][e] = res_load ? cur.res[t][e] : 0.f;
     }
+    const int64_t pos = st * 16 + r;
+    if (pos < npos) {
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        float o[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = res[t][e] + static_cast<float>(bf16(acc[t][e] * sig[t][e]));
+        rowstep::store4f<TOUT>(out + pos * K + 16 * t + 4 * g, o);
+      }
+    }
+    cur = next;
   }
 }
 
@@ -276,16 +284,19 @@ int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
 }
 
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s) {
-  const int64_t panels = ceil_div(int64_t(a.n) * a.n, ROWS);
+  const int64_t steps = ceil_div(int64_t(a.n) * a.n, 16);
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(steps, 8))));
   KernelTimer timer("trimul_output", s);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    trimul_output_kernel<bf16, bf16><<<dim3(panels), 256, 0, s>>>(a);
+    trimul_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
   else if (pair_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    trimul_output_kernel<bf16, float><<<dim3(panels), 256, 0, s>>>(a);
+    trimul_output_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
   else if (pair_dtype == XFH_F32 && out_dtype == XFH_F32)
-    trimul_output_kernel<float, float><<<dim3(panels), 256, 0, s>>>(a);
+    trimul_output_kernel<float, float><<<grid, 512, 0, s>>>(a);
   else
-    trimul_output_kernel<float, bf16><<<dim3(panels), 256, 0, s>>>(a);
+    trimul_output_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
   return check_launch("trimul_output");
 }
 
