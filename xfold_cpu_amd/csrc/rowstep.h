@@ -31,10 +31,10 @@ __host__ __device__ constexpr int kperm(int ks, int g, int j) {
   return j < 4 ? 32 * ks + 4 * g + j : 32 * ks + 16 + 4 * g + (j - 4);
 }
 
-// Copies W ([128][128] bf16, row-major) into LDS with the chunk swizzle; `permuted`
+// Copies W ([rows][128] bf16, row-major) into LDS with the chunk swizzle; `permuted`
 // reorders each row's input channels to kperm order. All threads of the workgroup take part.
-__device__ __forceinline__ void load_weight(const bf16 *__restrict__ w, bf16 *dst, bool permuted) {
-  for (int i = threadIdx.x; i < C * 16; i += blockDim.x) {
+__device__ __forceinline__ void load_weight(const bf16 *__restrict__ w, bf16 *dst, bool permuted, int rows = C) {
+  for (int i = threadIdx.x; i < rows * 16; i += blockDim.x) {
     const int n = i >> 4, c = i & 15;              // destination row, logical chunk
     const int ks = c >> 2, g = c & 3;
     bf16x8 v;
@@ -53,7 +53,8 @@ __device__ __forceinline__ void load_weight(const bf16 *__restrict__ w, bf16 *ds
   }
 }
 
-// A fragment of W for output tile t, k-step ks (lane: row 16 t + l % 16, chunk 4 ks + g).
+// Fragment of W for output tile t, k-step ks (lane: row 16 t + l % 16, chunk 4 ks + g):
+// the A operand of out^T = W . x^T, or the B operand of out = x . W^T (same lane layout).
 __device__ __forceinline__ bf16x8 weight_frag(const bf16 *w_lds, int t, int ks) {
   const int lane = threadIdx.x & 63, r = lane & 15, g = lane >> 4;
   const int n = 16 * t + r;
@@ -67,6 +68,14 @@ __device__ __forceinline__ void gemm_t(const bf16 *w_lds, const bf16x8 (&x)[4], 
   for (int t = 0; t < 8; ++t)
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) acc[t] = mfma16(weight_frag(w_lds, t, ks), x[ks], acc[t]);
+}
+
+// out tile: acc (+)= sum_ks x[ks] . W(t, ks) — rows are positions, columns the 16 output
+// channels of tile t; a lane ends up with 4 consecutive positions (4 g .. +3) of channel
+// 16 t + l % 16.
+__device__ __forceinline__ void gemm_n(const bf16 *w_lds, int t, const bf16x8 (&x)[4], f32x4 &acc) {
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) acc = mfma16(x[ks], weight_frag(w_lds, t, ks), acc);
 }
 
 // Sum over the four lanes of one position (l, l ^ 16, l ^ 32, l ^ 48). The swap results

@@ -8,8 +8,9 @@
 //       times sigmoid(gating_linear(LN_in(z))) (recomputed from z, which this kernel reads
 //       anyway for the residual) -> z += update (or update stored).
 //
-// trimul_project is a row-panel kernel (panel.h, 128 pair positions per workgroup);
-// trimul_output works on register-resident rows (rowstep.h).
+// trimul_project is a row-panel kernel (panel.h, 128 pair positions per workgroup, so each
+// channel's row of the operand layout is written 256 bytes at a time); trimul_output works
+// on register-resident rows (rowstep.h).
 #include <algorithm>
 
 #include "common.h"
