@@ -326,7 +326,22 @@ def test_grid_self_attention_mask_cases(device, transpose, sharp):
     assert_parity_bf16(got, floor if sharp else want, "grid attention mask cases (bf16 store)")
 
 
-@pytest.mark.parametrize("c,f,rows", [(128, 4, (33, 17)), (384, 4, (50,)), (16, 4, (2, 5))])
+@pytest.mark.parametrize("rows", [(37, 41), (300, 290)])
+def test_transition_in_place(device, rows):
+    """The pair stack's use: bf16 pair += transition(pair), in place."""
+    announce("transition in place", rows)
+    ref, hip = pair_of("Transition", dict(c_x=128, num_intermediate_factor=4), seed=7)
+    torch.manual_seed(7)
+    x = torch.randn(*rows, 128).bfloat16()
+    with torch.no_grad():
+        want = x.float() + ref(x.float())
+    y = x.to(device)
+    with torch.inference_mode(), autocast(True):
+        hnn.transition_hip(hip, y, accumulate_into=y)
+    assert_parity_bf16(y, want, "transition in place (bf16)")
+
+
+@pytest.mark.parametrize("c,f,rows", [(128, 4, (33, 17)), (128, 4, (300, 290)), (384, 4, (50,)), (16, 4, (2, 5))])
 @pytest.mark.parametrize("bf16", [False, True])
 def test_transition(device, c, f, rows, bf16):
     announce("transition", c, f, rows, bf16)
