@@ -31,17 +31,28 @@ PEAK_BF16_TFLOPS = 2500.0
 PEAK_HBM_GBS = 8000.0
 
 
+# (timed steps, warm-up steps) per configuration; a step is one forward of the workload.
+DEFAULT_STEPS = {"C1": (200, 50), "C2": (200, 50), "C3": (10, 3), "C4": (10, 3), "C5": (20, 5)}
+
+
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=10)
-    p.add_argument("--warmup", type=int, default=3)
+    p.add_argument("--steps", type=int, default=None,
+                   help="timed steps (default per config: enough to reach steady clocks)")
+    p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration-mb", type=int, default=0,
                    help="after the run, copy a buffer of this many MiB once (a plain copy kernel of "
                         "known size whose FETCH_SIZE/WRITE_SIZE counters calibrate the traffic figure)")
-    return p.parse_args()
+    args = p.parse_args()
+    # A single N=384 block is ~0.7 ms: a few warm-up blocks leave the GPU below its steady
+    # clock, so the small configurations warm up and time over many blocks.
+    steps, warmup = DEFAULT_STEPS[args.config]
+    args.steps = steps if args.steps is None else args.steps
+    args.warmup = warmup if args.warmup is None else args.warmup
+    return args
 
 
 def log(*a):
@@ -184,7 +195,8 @@ def main():
     step, blocks, workload, cfg = build_workload(args.config, device)
     for i in range(args.warmup):
         step()
-        log(f"warmup {i + 1}/{args.warmup}")
+        if i == 0 or i + 1 == args.warmup:
+            log(f"warmup {i + 1}/{args.warmup}")
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(device)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -104,7 +104,7 @@ static GemmArgs gemm_args(const void *A, int64_t lda, const void *B, int64_t ldb
 
 // ------------------------------------------------------------------ triangle multiplication
 struct TriMulPlan {
-  void *normed, *proj, *gate, *left, *right, *contracted, *centered, *gating, *packed;
+  void *normed, *proj, *gate, *left, *right, *contracted, *centered, *gating;
 };
 
 static bool trimul_fast_path(int64_t c, int dtype) { return dtype == XFH_BF16 && c == 128; }
@@ -113,7 +113,6 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
   const int64_t es = dsize(dtype), plane = n * n;
   std::memset(&p, 0, sizeof(p));
   if (trimul_fast_path(c, dtype)) {
-    p.packed = cv.take(4 * c * c * es);
     p.left = cv.take(n * contraction_ld(n) * c * es);
     p.right = cv.take(n * contraction_ld(n) * c * es);
     p.contracted = cv.take(plane * c * es);
@@ -336,11 +335,10 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
   hipStream_t s = as_stream(stream);
   const int64_t plane = n * n;
   if (trimul_fast_path(c, dtype)) {
-    XFH_TRY(trimul_pack(proj_w, gate_w, int(c), p.packed, s));
     TriProjectArgs pa;
     pa.pair = pair; pa.mask = mask; pa.mask_dtype = mask_dtype;
     pa.ln_w = left_w; pa.ln_b = left_b; pa.eps = left_eps;
-    pa.w_packed = static_cast<const bf16 *>(p.packed);
+    pa.w_proj = static_cast<const bf16 *>(proj_w); pa.w_gate = static_cast<const bf16 *>(gate_w);
     pa.left = static_cast<bf16 *>(p.left); pa.right = static_cast<bf16 *>(p.right);
     pa.n = int(n); pa.ld = int(contraction_ld(n)); pa.outgoing = outgoing;
     XFH_TRY(trimul_project(pa, pair_dtype, s));
@@ -413,7 +411,8 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
   if (grid_fast_path(n, c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
-    XFH_TRY(grid_pack(q_w, k_w, v_w, bias_w, int(c), int(heads), p.packed, s));
+    XFH_TRY(grid_prepare(q_w, k_w, v_w, bias_w, int(c), int(heads), p.packed, mask, mask_dtype, n,
+                         npad / 64, p.maskbits, s));
     GridProjectArgs pa;
     pa.pair = pair; pa.n = int(n); pa.heads = int(heads); pa.transpose = transpose;
     pa.ln_w = norm_w; pa.ln_b = norm_b; pa.eps = eps;
@@ -422,7 +421,6 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
     pa.q = static_cast<bf16 *>(p.qh); pa.k = static_cast<bf16 *>(p.kh); pa.vt = static_cast<bf16 *>(p.vt);
     pa.bias = p.bias_t; pa.npad = int(npad);
     XFH_TRY(grid_project(pa, pair_dtype, s));
-    XFH_TRY(grid_mask(mask, mask_dtype, n, npad / 64, p.maskbits, s));
     GridAttentionArgs ga;
     ga.q = static_cast<const bf16 *>(p.qh);
     ga.k = static_cast<const bf16 *>(p.kh);

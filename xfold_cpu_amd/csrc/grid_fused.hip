@@ -8,7 +8,7 @@
 //       The bias comes from the un-transposed pair in both directions.
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
 //       the residual) -> (gate * o) Wout^T -> z += update (or update stored).
-//   grid_mask_words: per batch row, one 64-bit word of kept keys per 64 keys.
+//   grid_prepare: the packed weight and the attention kernel's kept-key words, one launch.
 #include <algorithm>
 
 #include "common.h"
@@ -251,10 +251,27 @@ __global__ __launch_bounds__(512, 1) void grid_output_kernel(GridOutputArgs a) {
   }
 }
 
-// One wavefront per 64-key word: lane i tests key w*64 + i, the ballot is the word.
-__global__ void grid_mask_words(const void *__restrict__ mask, int mask_dtype, int64_t n, int64_t nblk,
-                                uint64_t *__restrict__ bits) {
-  const int64_t word = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+// Blocks [0, pack_blocks): packed weight [3c + 64][c] (q, k, v, then the bias rows
+// zero-padded to 64), one element per thread. The rest: one wavefront per 64-key word,
+// lane i tests key w*64 + i and the ballot is the word.
+__global__ void grid_prepare_kernel(const bf16 *__restrict__ wq, const bf16 *__restrict__ wk,
+                                    const bf16 *__restrict__ wv, const bf16 *__restrict__ wb, int c,
+                                    int heads, bf16 *__restrict__ packed, int64_t pack_blocks,
+                                    const void *__restrict__ mask, int mask_dtype, int64_t n, int64_t nblk,
+                                    uint64_t *__restrict__ bits) {
+  if (blockIdx.x < pack_blocks) {
+    const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
+    if (idx >= int64_t(PACKED_ROWS) * c) return;
+    const int r = int(idx / c), k = int(idx % c);
+    bf16 v = bf16(0.0f);
+    if (r < c) v = wq[int64_t(r) * c + k];
+    else if (r < 2 * c) v = wk[int64_t(r - c) * c + k];
+    else if (r < 3 * c) v = wv[int64_t(r - 2 * c) * c + k];
+    else if (r - 3 * c < heads) v = wb[int64_t(r - 3 * c) * c + k];
+    packed[idx] = v;
+    return;
+  }
+  const int64_t word = (int64_t(blockIdx.x) - pack_blocks) * 4 + (threadIdx.x >> 6);
   if (word >= n * nblk) return;
   const int64_t b = word / nblk, w = word % nblk;
   const int64_t k = w * 64 + (threadIdx.x & 63);
@@ -263,39 +280,19 @@ __global__ void grid_mask_words(const void *__restrict__ mask, int mask_dtype, i
   if ((threadIdx.x & 63) == 0) bits[word] = ballot;
 }
 
-// Packed [3c + 64][c]: q, k, v weights, then the bias projection rows (zero-padded to 64).
-__global__ void grid_pack_kernel(const bf16 *__restrict__ wq, const bf16 *__restrict__ wk,
-                                 const bf16 *__restrict__ wv, const bf16 *__restrict__ wb, int c,
-                                 int heads, bf16 *__restrict__ packed) {
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = int64_t(PACKED_ROWS) * c;
-  if (idx >= total) return;
-  const int r = int(idx / c), k = int(idx % c);
-  bf16 v = bf16(0.0f);
-  if (r < c) v = wq[int64_t(r) * c + k];
-  else if (r < 2 * c) v = wk[int64_t(r - c) * c + k];
-  else if (r < 3 * c) v = wv[int64_t(r - 2 * c) * c + k];
-  else if (r - 3 * c < heads) v = wb[int64_t(r - 3 * c) * c + k];
-  packed[idx] = v;
-}
-
 }  // namespace
 
 int64_t grid_packed_rows() { return PACKED_ROWS; }
 
-int grid_pack(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
-              void *packed, hipStream_t s) {
-  const int64_t total = int64_t(PACKED_ROWS) * c;
-  grid_pack_kernel<<<dim3(ceil_div(total, 256)), 256, 0, s>>>((const bf16 *)wq, (const bf16 *)wk,
-                                                               (const bf16 *)wv, (const bf16 *)wb, c, heads,
-                                                               (bf16 *)packed);
-  return check_launch("grid_pack");
-}
-
-int grid_mask(const void *mask, int mask_dtype, int64_t n, int64_t nblk, uint64_t *bits, hipStream_t s) {
-  const int64_t words = n * nblk;
-  grid_mask_words<<<dim3(ceil_div(words, 4)), 256, 0, s>>>(mask, mask_dtype, n, nblk, bits);
-  return check_launch("grid_mask_words");
+int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
+                 void *packed, const void *mask, int mask_dtype, int64_t n, int64_t nblk,
+                 uint64_t *bits, hipStream_t s) {
+  const int64_t pack_blocks = ceil_div(int64_t(PACKED_ROWS) * c, 256);
+  const int64_t word_blocks = ceil_div(n * nblk, 4);
+  grid_prepare_kernel<<<dim3(pack_blocks + word_blocks), 256, 0, s>>>(
+      (const bf16 *)wq, (const bf16 *)wk, (const bf16 *)wv, (const bf16 *)wb, c, heads, (bf16 *)packed,
+      pack_blocks, mask, mask_dtype, n, nblk, bits);
+  return check_launch("grid_prepare");
 }
 
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {

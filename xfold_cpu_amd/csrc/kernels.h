@@ -48,7 +48,7 @@ int attention(const AttentionArgs &a, int dtype, hipStream_t s);
 struct GridAttentionArgs {
   const bf16 *q, *k, *vt;
   const float *bias;
-  const uint64_t *maskbits;
+  const uint64_t *maskbits;  // [B][Npad/64], see grid_prepare
   bf16 *out;
   int64_t osb, ost;          // out element (b, t, h, d) at out[b*osb + t*ost + h*32 + d]
   int B, H, N, Npad, Nblk;
@@ -59,7 +59,7 @@ struct GridProjectArgs {
   int n, heads, transpose;
   const float *ln_w, *ln_b;
   float eps;
-  const bf16 *w_packed;      // [3c + 64][c], see grid_pack
+  const bf16 *w_packed;      // [3c + 64][c], see grid_prepare
   float qscale;              // d^-0.5 * log2(e)
   bf16 *q, *k, *vt;
   float *bias;
@@ -75,9 +75,12 @@ struct GridOutputArgs {
   int accumulate, n;
 };
 int64_t grid_packed_rows();
-int grid_pack(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
-              void *packed, hipStream_t s);
-int grid_mask(const void *mask, int mask_dtype, int64_t n, int64_t nblk, uint64_t *bits, hipStream_t s);
+// One launch: the packed [q | k | v | bias] weight of grid_project and the 64-bit
+// kept-key words of the attention kernel (bit s of word b*nblk + s/64 set iff key s < n of
+// batch row b is kept, mask[b*n + s] != 0).
+int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
+                 void *packed, const void *mask, int mask_dtype, int64_t n, int64_t nblk,
+                 uint64_t *bits, hipStream_t s);
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s);
 int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 int64_t grid_attention_pad(int64_t n);
@@ -91,7 +94,7 @@ struct TriProjectArgs {
   int mask_dtype;
   const float *ln_w, *ln_b;
   float eps;
-  const bf16 *w_packed;      // [4c][c], see trimul_pack
+  const bf16 *w_proj, *w_gate;  // [2c][c] each (nn.Linear layout)
   bf16 *left, *right;        // [c][n][ld] contraction operands (contraction_ld), zero-padded
   int n, ld, outgoing;
 };
@@ -126,7 +129,6 @@ struct ContractionArgs {
 };
 int64_t contraction_ld(int64_t n);
 int contraction(const ContractionArgs &a, hipStream_t s);
-int trimul_pack(const void *proj, const void *gate, int c, void *packed, hipStream_t s);
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s);
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 

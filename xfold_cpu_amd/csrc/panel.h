@@ -142,6 +142,21 @@ __device__ __forceinline__ void fetch_b(const bf16 *W, int n0, int n_total, BSta
   }
 }
 
+// The same staging for a weight given row by row: row_ptr(r) is the address of row r's
+// 128 inputs, or nullptr for a zero row (lets a kernel read several nn.Linear weights as
+// one packed matrix without packing them first).
+template <typename RowPtr>
+__device__ __forceinline__ void fetch_rows(RowPtr row_ptr, int n0, BStage &st) {
+  const int tid = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int idx = tid + i * 256;
+    const int r = idx >> 4, c = (idx & 15) * 8;
+    const bf16 *src = row_ptr(n0 + r);
+    st.v[i] = src ? *reinterpret_cast<const uint4 *>(src + c) : make_uint4(0, 0, 0, 0);
+  }
+}
+
 __device__ __forceinline__ void stash_b(const BStage &st, bf16 *b_tile) {
   const int tid = threadIdx.x;
 #pragma unroll

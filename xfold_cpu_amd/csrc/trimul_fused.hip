@@ -1,7 +1,7 @@
 // Fused triangle-multiplication kernels (bf16 compute, c = 128), around the per-channel
 // contraction (xfold/nn/triangle_multiplication.py:71-105):
 //
-//   trimul_project: LN_in(z) -> [projection | gate] (one GEMM over a packed weight) ->
+//   trimul_project: LN_in(z) -> [projection | gate] (one GEMM over both weights' rows) ->
 //       mask * proj * sigmoid(gate) -> channel 2k = a_k, 2k+1 = b_k -> written channel-major
 //       in the contraction's operand layouts (left/right, see triangle.hip).
 //   trimul_output: centre LN over the channel-major contraction result -> output_projection,
@@ -54,9 +54,15 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
   __syncthreads();
   AFrags af;
   load_a_frags(lds_a, wm, af);
+  // Weight row r of chunk j = r / 64 (64 rows): projection rows 32j..32j+15, gate rows
+  // 32j..32j+15, projection rows 32j+16..32j+31, gate rows 32j+16..32j+31.
+  auto wrow = [&](int r) -> const bf16 * {
+    const int j = r >> 6, s4 = (r >> 4) & 3, i = r & 15;
+    return ((s4 & 1) ? a.w_gate : a.w_proj) + (32 * j + (s4 >= 2 ? 16 : 0) + i) * K;
+  };
   BStage st;
   const int nout = 4 * K;                          // projection + gate, 2c each
-  fetch_b(a.w_packed, 0, nout, st);
+  fetch_rows(wrow, 0, st);
   __syncthreads();                                 // A tile consumed; reuse as B buffers
   stash_b(st, bbuf(0));
   __syncthreads();
@@ -65,7 +71,7 @@ __global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a
   const int64_t plane = int64_t(n) * a.ld;
   const int chunks = nout / CHUNK;
   for (int j = 0; j < chunks; ++j) {
-    if (j + 1 < chunks) fetch_b(a.w_packed, (j + 1) * CHUNK, nout, st);
+    if (j + 1 < chunks) fetch_rows(wrow, (j + 1) * CHUNK, st);
     f32x4 acc[4][2];
     zero(acc);
     mma_chunk(af, bbuf(j), wn, acc);
@@ -251,28 +257,7 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
   }
 }
 
-// Packed [4c][c] weight: chunk j (64 rows) = projection rows 32j..32j+15, gate rows
-// 32j..32j+15, projection rows 32j+16..32j+31, gate rows 32j+16..32j+31.
-__global__ void trimul_pack_kernel(const bf16 *__restrict__ proj, const bf16 *__restrict__ gate,
-                                   int c, bf16 *__restrict__ packed) {
-  const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t total = int64_t(4) * c * c;
-  if (idx >= total) return;
-  const int r = int(idx / c), k = int(idx % c);
-  const int j = r / 64, s = (r % 64) / 16, i = r % 16;
-  const int src_row = 32 * j + (s >= 2 ? 16 : 0) + i;
-  const bf16 *src = (s & 1) ? gate : proj;
-  packed[idx] = src[int64_t(src_row) * c + k];
-}
-
 }  // namespace
-
-int trimul_pack(const void *proj, const void *gate, int c, void *packed, hipStream_t s) {
-  const int64_t total = int64_t(4) * c * c;
-  trimul_pack_kernel<<<dim3(ceil_div(total, 256)), 256, 0, s>>>((const bf16 *)proj, (const bf16 *)gate, c,
-                                                                 (bf16 *)packed);
-  return check_launch("trimul_pack");
-}
 
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
   const int64_t panels = int64_t(a.n) * ceil_div(a.n, ROWS);
