@@ -44,8 +44,9 @@ def parse():
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--copy-calibration-mb", type=int, default=0,
-                   help="after the run, copy a buffer of this many MiB once (a plain copy kernel of "
-                        "known size whose FETCH_SIZE/WRITE_SIZE counters calibrate the traffic figure)")
+                   help="after the run, read and write a buffer of this many MiB once (a plain copy "
+                        "kernel of known size whose FETCH_SIZE/WRITE_SIZE counters calibrate the "
+                        "traffic figure)")
     args = p.parse_args()
     # A single N=384 block is ~0.7 ms: a few warm-up blocks leave the GPU below its steady
     # clock, so the small configurations warm up and time over many blocks.
@@ -114,6 +115,13 @@ def build_workload(cfg_name, device):
     return step, 1, workload, cfg
 
 
+# HBM bytes per grid_attention_kernel launch, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
+# the same workload (bench.py --config C2|C3 --copy-calibration-mb 512), calibrated against that
+# 512 MiB read+write kernel: bytes = (2 x FETCH_SIZE + WRITE_SIZE) KiB x 1024. Counters cannot be
+# read inside this process, so the figure is the recorded measurement for the configuration.
+ATTENTION_TRAFFIC_BYTES = {384: 168.25e6, 768: 1037.9e6}
+
+
 def kernel_roofline(step, n, steps):
     """Average duration of the dominant kernel (triangle attention core: B=N rows, 4 heads
     x 32, N x N keys, pair bias and 2-D key mask) inside the block workload, from HIP events
@@ -139,7 +147,7 @@ def kernel_roofline(step, n, steps):
     achieved = flops / (ms * 1e-3) / 1e12
     return {"kernel": "grid_attention_kernel (triangle attention core)", "bound": "mfma",
             "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": None,
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": ATTENTION_TRAFFIC_BYTES.get(n),
             "avg_launch_ms": round(ms, 4), "launches": launches, "flops_per_launch": flops,
             "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}
 
@@ -222,11 +230,13 @@ def main():
         log(f"cpu baseline: {base}")
 
     if args.copy_calibration_mb:
+        # One elementwise kernel (bitwise_not, a name no other kernel of the run has) that
+        # reads and writes exactly this many MiB.
         src = torch.ones(args.copy_calibration_mb << 20, dtype=torch.uint8, device=device)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        torch.bitwise_not(src, out=dst)
         torch.cuda.synchronize()
-        log(f"copy calibration: {args.copy_calibration_mb} MiB copied")
+        log(f"copy calibration: {args.copy_calibration_mb} MiB read and written")
 
     dtype = "bf16" if cfg["dtype"] == "bf16" else "fp32"
     line = {

@@ -149,7 +149,7 @@ static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t
     const int64_t npad = grid_attention_pad(n);
     p.packed = cv.take(grid_packed_rows() * c * es);
     p.qh = cv.take(plane * c * es);
-    p.kh = cv.take(plane * c * es);
+    p.kh = cv.take(n * c * npad * es);
     p.vt = cv.take(n * c * npad * es);
     p.bias_t = static_cast<float *>(cv.take(heads * n * npad * 4));
     p.maskbits = static_cast<uint64_t *>(cv.take(n * (npad / 64) * 8));

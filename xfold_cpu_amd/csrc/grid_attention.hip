@@ -8,7 +8,7 @@
 //
 // Operand layouts (written by grid_project):
 //   q   [B][H][N][32] bf16, pre-multiplied by d^-0.5 * log2(e)
-//   k   [B][H][N][32] bf16
+//   k   [B][H][Npad][32] bf16, zero for keys >= N
 //   vt  [B][H][32][Npad] bf16, zero for keys >= N; inside every run of 32 keys, position
 //       8g + j holds key 4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4), the key order of a
 //       lane's P^T fragment
@@ -197,10 +197,23 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
   // operand read hit 16 distinct bank groups:
   //   K:   slot s of key j holds its 8-element chunk s ^ ((j >> 2) & 3)
   //   V^T: slot s of row d holds its 8-element chunk s ^ ((d >> 1) & 7)
-  // Keys >= N of K are read from key N-1 (their logits are masked); V^T is zero there.
+  // K and V^T are zero for keys >= N (their logits are masked). Each lane's source is a
+  // per-(row, block) uniform base plus a per-lane byte offset fixed for the kernel.
   // From the first block that needs the mask on, wavefront r < R also turns row r's mask
   // word into the additive mask row (0 or -1e30), before the loads: an LDS store after
   // them would wait for them to land.
+  uint32_t piece_off[8 / W];                         // bytes, per piece of this wavefront
+#pragma unroll
+  for (int j = 0; j < 8 / W; ++j) {
+    const int piece = wave + j * W, i = piece & 3;
+    if (piece < 4) {
+      const int key = i * 16 + (lane >> 2), kchunk = (lane & 3) ^ ((lane >> 4) & 3);
+      piece_off[j] = uint32_t(key * GD + kchunk * 8) * 2;
+    } else {
+      const int d = i * 8 + (lane >> 3), vchunk = (lane & 7) ^ ((d >> 1) & 7);
+      piece_off[j] = uint32_t(d * a.Npad + vchunk * 8) * 2;
+    }
+  }
   auto issue = [&](int kb, int stage) {
     if (kb >= first_masked && wave < R) {
       const uint64_t word = words[wave][kb];
@@ -215,17 +228,11 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       for (int j = 0; j < 8 / W; ++j) {
         const int piece = wave + j * W;              // 0..3: K keys 16 i.., 4..7: V^T rows 8 i..
         const int i = piece & 3;
-        if (piece < 4) {
-          const int key = kb * GKB + i * 16 + (lane >> 2);
-          const int kchunk = (lane & 3) ^ ((lane >> 4) & 3);
-          const bf16 *src = a.k + (bh * a.N + (key < a.N ? key : a.N - 1)) * GD + kchunk * 8;
-          __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(kbuf(stage, r) + i * 16 * GD), 16, 0, 0);
-        } else {
-          const int d = i * 8 + (lane >> 3);
-          const int vchunk = (lane & 7) ^ ((d >> 1) & 7);
-          const bf16 *src = a.vt + (bh * GD + d) * a.Npad + int64_t(kb) * GKB + vchunk * 8;
-          __builtin_amdgcn_global_load_lds((global_void *)src, (lds_void *)(vbuf(stage, r) + i * 8 * GKB), 16, 0, 0);
-        }
+        const char *base = piece < 4
+            ? reinterpret_cast<const char *>(a.k + (bh * a.Npad + int64_t(kb) * GKB) * GD)
+            : reinterpret_cast<const char *>(a.vt + bh * GD * a.Npad + int64_t(kb) * GKB);
+        bf16 *dst = piece < 4 ? kbuf(stage, r) + i * 16 * GD : vbuf(stage, r) + i * 8 * GKB;
+        __builtin_amdgcn_global_load_lds((global_void *)(base + piece_off[j]), (lds_void *)dst, 16, 0, 0);
       }
     }
   };

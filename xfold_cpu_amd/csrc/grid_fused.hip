@@ -2,8 +2,8 @@
 // c = 128, 4 heads x 32), following GridSelfAttention.forward (xfold/nn/attention.py:80-105):
 //
 //   grid_project: LN(z) -> one GEMM over a packed [q | k | v | bias] weight -> q scaled by
-//       d^-0.5 * log2(e), k, v^T (zero beyond n, keys permuted in runs of 32) and the fp32
-//       pair bias (times log2(e)),
+//       d^-0.5 * log2(e), k (rows up to npad, zero beyond n), v^T (zero beyond n, keys
+//       permuted in runs of 32) and the fp32 pair bias (times log2(e)),
 //       each written straight into the attention kernel's layout (grid_attention.hip).
 //       The bias comes from the un-transposed pair in both directions.
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
@@ -96,16 +96,20 @@ __global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a)
             stage[(wm * 64 + mt * 16 + grp * 4 + e) * CPITCH + wn * 32 + nt * 16 + col] =
                 bf16(acc[mt][nt][e] * scale);
       __syncthreads();
+      // q rows: [b][h][n][32]; k rows: [b][h][npad][32], zero for n <= t < npad (the
+      // attention kernel loads whole 64-key blocks of k without bounds).
       bf16 *dst = kind == 0 ? a.q : a.k;
+      const int rows = kind == 0 ? n : a.npad;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int idx = tid + i * 256;              // 128 rows x 8 chunks of 8
         const int r = idx >> 3, c = (idx & 7) * 8;
         const int t = t0 + r;
-        if (t >= n) continue;
+        if (t >= rows) continue;
         const int h = (j & 1) * 2 + c / HD;
-        *reinterpret_cast<bf16x8 *>(dst + ((int64_t(b) * H + h) * n + t) * HD + (c % HD)) =
-            *reinterpret_cast<const bf16x8 *>(&stage[r * CPITCH + c]);
+        bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[r * CPITCH + c]);
+        if (t >= n) v = bf16x8{};
+        *reinterpret_cast<bf16x8 *>(dst + ((int64_t(b) * H + h) * rows + t) * HD + (c % HD)) = v;
       }
     } else {
       // v: stage transposed [64 cols][128 rows] then [b][h][d][npad] rows, zero beyond n.
