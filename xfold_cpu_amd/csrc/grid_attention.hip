@@ -49,8 +49,8 @@ constexpr int GKB = 64;              // keys per block
 constexpr int K_ELEMS = GKB * GD;    // K tile of one row: [64 keys][32], 64 B per key
 constexpr int V_ELEMS = GD * GKB;    // V^T tile of one row: [32 d][64 keys], 128 B per d
 constexpr int MB_ZERO = 64;          // zeros read by the lanes that supply no mask value
-// Mask words of a row group are kept in LDS: a global read inside the key loop would wait
-// (vmcnt) for the block prefetch issued before it.
+// Mask words of a row group are kept in registers (lane w holds word w of each row): a
+// global read inside the key loop would wait (vmcnt) for the block prefetch issued before it.
 constexpr int kMaxKeyBlocks = 64;    // N <= 4096
 constexpr float kRescaleSlack = 8.0f;
 // Initial running maximum: finite, so that a block whose keys are all masked (logits near
@@ -110,7 +110,6 @@ template <class S>
 __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAttentionArgs a) {
   constexpr int R = S::R, W = S::W, TQ = S::TQ, GQ = S::Q, GT = S::T, STAGE = S::STAGE;
   __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE + MB_ZERO];
-  __shared__ uint64_t words[R][kMaxKeyBlocks];       // the group's mask words
   auto kbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + r * K_ELEMS; };
   auto vbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + R * K_ELEMS + r * V_ELEMS; };
   auto mbuf = [&](int stage, int r) -> bf16 * {
@@ -151,29 +150,15 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       m[r][tq] = kInitialMax;
     }
   }
-  if (tid < MB_ZERO) mzero[tid] = bf16(0.0f);
-  for (int i = tid; i < R * a.Nblk; i += GT) {
-    const int r = i / a.Nblk, w = i % a.Nblk, b = rg * R + r;
-    words[r][w] = b < a.B ? a.maskbits[int64_t(b) * a.Nblk + w] : 0;
-  }
-  __syncthreads();                                   // words, mzero
-  // Row status from the mask words, in every wavefront at once (lane w reads word w):
-  // a row is present if b < B, active if it also keeps some key; first_masked is the
-  // first key block in which some row of the group does not keep all 64 keys.
-  bool all_masked[R];
-  int active = 0, present = 0;
-  uint64_t full_blocks = a.Nblk == 64 ? ~0ull : ((1ull << a.Nblk) - 1);
+  if (tid < MB_ZERO) mzero[tid] = bf16(0.0f);       // (LDS stores go before any direct load)
+  // Lane w holds word w (key block w) of each row of the group.
+  uint64_t wr[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint64_t w = lane < a.Nblk ? words[r][lane] : 0;
-    const bool any = __ballot(w != 0) != 0;
-    full_blocks &= __ballot(w == ~0ull);
-    const bool here = rg * R + r < a.B;
-    all_masked[r] = here && !any;
-    if (here) present |= 1 << r;
-    if (here && any) active |= 1 << r;
+    const int b = rg * R + r;
+    wr[r] = b < a.B && lane < a.Nblk ? a.maskbits[int64_t(b) * a.Nblk + lane] : 0;
   }
-  const int first_masked = full_blocks == ~0ull ? a.Nblk : __builtin_ctzll(~full_blocks);
+
 
   // Swizzled LDS offsets of this lane's K fragment (key kt*16 + col, chunk grp) and V^T
   // fragments (row t*16 + col, chunk 4c + grp); the mask fragment (key kt*16 + col in
@@ -214,11 +199,22 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       piece_off[j] = uint32_t(d * a.Npad + vchunk * 8) * 2;
     }
   }
-  auto issue = [&](int kb, int stage) {
+  // Row status, set in the prologue from the mask words (block 0's loads go out before
+  // them): a row is present if b < B, active if it also keeps some key; first_masked is the
+  // first key block in which some row of the group does not keep all 64 keys.
+  bool all_masked[R];
+  int active = 0, present = 0, first_masked = 0;
+  uint32_t row_lo = 0, row_hi = 0;                   // this wavefront's row word, lane w = block w
+  // Additive mask row (0 or -1e30 per key) of block kb for wavefront r < R's row.
+  auto mask_row = [&](int kb, int stage) {
     if (kb >= first_masked && wave < R) {
-      const uint64_t word = words[wave][kb];
+      const uint32_t hi = uint32_t(__builtin_amdgcn_readlane(int(row_hi), kb));
+      const uint32_t lo = uint32_t(__builtin_amdgcn_readlane(int(row_lo), kb));
+      const uint64_t word = (uint64_t(hi) << 32) | lo;
       mbuf(stage, wave)[lane] = ((word >> lane) & 1ull) ? bf16(0.0f) : bf16(kMaskedLogit);
     }
+  };
+  auto issue_kv = [&](int kb, int stage) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int b = rg * R + r;
@@ -235,6 +231,12 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
         __builtin_amdgcn_global_load_lds((global_void *)(base + piece_off[j]), (lds_void *)dst, 16, 0, 0);
       }
     }
+  };
+  // Block kb into a stage: the mask row first (an LDS store after the direct loads would wait
+  // for them), then K and V^T.
+  auto issue = [&](int kb, int stage) {
+    mask_row(kb, stage);
+    issue_kv(kb, stage);
   };
   // Waits for this thread's outstanding global loads (LDS transfers included).
   auto drain = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
@@ -368,9 +370,31 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
     __syncthreads();
   };
 
-  issue(0, 0);
+  // Block 0's K/V and bias go out together with the q and mask-word loads above; one wait.
+  issue_kv(0, 0);
   load_bias(0);
   drain();
+  // Row status from the mask words, in every wavefront at once.
+  uint64_t full_blocks = a.Nblk == 64 ? ~0ull : ((1ull << a.Nblk) - 1);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint64_t w = wr[r];
+    const bool any = __ballot(w != 0) != 0;
+    full_blocks &= __ballot(w == ~0ull);
+    const bool here = rg * R + r < a.B;
+    all_masked[r] = here && !any;
+    if (here) present |= 1 << r;
+    if (here && any) active |= 1 << r;
+  }
+  first_masked = full_blocks == ~0ull ? a.Nblk : __builtin_ctzll(~full_blocks);
+  // This wavefront's row word (wavefront r < R writes row r's additive mask rows).
+  uint64_t row_word = 0;
+#pragma unroll
+  for (int r = 0; r < R; ++r)
+    if (wave == r) row_word = wr[r];
+  row_lo = uint32_t(row_word);
+  row_hi = uint32_t(row_word >> 32);
+  mask_row(0, 0);                                    // after the wait: no extra wait
   __syncthreads();
 
   using T_ = std::true_type;
