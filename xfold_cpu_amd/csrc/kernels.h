@@ -21,6 +21,10 @@ struct GemmArgs {
 };
 
 int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s);
+// bf16-input GEMM with a direct-load LDS ring (gemm_ring.hip); gemm_nt routes to it when
+// gemm_ring_supported (k a multiple of 32, 16-byte aligned operand rows, 4-aligned output).
+bool gemm_ring_supported(const GemmArgs &p, int out_dtype);
+int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s);
 int glu_pack(const void *w, int64_t f, int64_t k, int dtype, void *packed, hipStream_t s);
 
 int layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, const float *w, const float *b,
