@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 1
+#define XFH_ABI_VERSION 2
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -103,11 +103,16 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
  * with bf16 inputs (fp32 accumulation is kept to the store). Semantics of
  * xfold/fastnn/attention.py:45-66: logits = (q*scale) k^T + bias; masked logits := -1e9;
  * softmax over keys; @ v. Replaces `dot_product_attention`
- * (af3_kernels/src/csrc/dot_product_attention.cpp:110-174, bindings.cpp:44-48). */
+ * (af3_kernels/src/csrc/dot_product_attention.cpp:110-174, bindings.cpp:44-48).
+ * With bf16 inputs and output, head dims <= 64, a bias shared by the batch entries and a
+ * mask that depends on the batch entry and key only (the single-track and diffusion
+ * shapes), a workspace of xfh_dot_product_attention_workspace_size(shape, dtype) bytes
+ * selects the pipelined kernel; other calls, or workspace = NULL, use the general one. */
+int64_t xfh_dot_product_attention_workspace_size(const int64_t *shape, int dtype);
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
                               void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
-                              float scale, void *stream);
+                              float scale, void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).
  * out (contiguous [n, n, c]) receives the update, or the update is added to it when

@@ -53,7 +53,7 @@ def test_invalid_arguments_fail_before_any_launch():
     strides = (ctypes.c_int64 * 20)()
     with pytest.raises(ValueError, match="dtype"):
         nh.call("xfh_dot_product_attention", None, None, None, 5, None, 2, None, 0, None, 1, shape,
-                strides, 1.0, None)
+                strides, 1.0, None, 0, None)
     lib = nh.load_library()
     assert "dtype" in lib.xfh_last_error().decode()
 

@@ -79,19 +79,6 @@ static bool float_dtype(int d) { return d == XFH_F32 || d == XFH_BF16; }
 static bool mask_dtype_ok(int d) { return d == XFH_F32 || d == XFH_BF16 || d == XFH_BOOL; }
 static int64_t dsize(int d) { return d == XFH_F32 ? 4 : d == XFH_BF16 ? 2 : 1; }
 
-// Bump allocator over a caller-provided workspace; 256-byte aligned slices.
-struct Carver {
-  char *base;
-  int64_t used = 0, cap;
-  Carver(void *b, int64_t c) : base(static_cast<char *>(b)), cap(c) {}
-  void *take(int64_t bytes) {
-    used = align_up(used, 256);
-    void *p = base ? base + used : nullptr;
-    used += bytes;
-    return p;
-  }
-};
-
 static GemmArgs gemm_args(const void *A, int64_t lda, const void *B, int64_t ldb, void *C,
                           int64_t ldc, int64_t M, int64_t N, int64_t K) {
   GemmArgs g;
@@ -278,10 +265,21 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
   return gemm_nt(g, 1, dtype, y_dtype, true, as_stream(stream));
 }
 
+int64_t xfh_dot_product_attention_workspace_size(const int64_t *shape, int dtype) {
+  if (!shape || !float_dtype(dtype)) return -1;
+  for (int i = 0; i < 6; ++i)
+    if (shape[i] < 0) return -1;
+  if (dtype != XFH_BF16) return 0;
+  AttentionArgs a;
+  std::memset(&a, 0, sizeof(a));
+  a.B = shape[0]; a.H = shape[1]; a.Q = shape[2]; a.K = shape[3]; a.D = shape[4]; a.Dv = shape[5];
+  return mha_workspace_size(a);
+}
+
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
                               void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
-                              float scale, void *stream) {
+                              float scale, void *workspace, int64_t workspace_bytes, void *stream) {
   XFH_REQUIRE(shape && strides, "dot_product_attention: null shape/strides");
   XFH_REQUIRE(float_dtype(dtype), "dot_product_attention: dtype must be f32/bf16");
   XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "dot_product_attention: bad mask dtype");
@@ -301,6 +299,11 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   a.scale = scale;
   if (a.B * a.H * a.Q * a.Dv == 0) return XFH_OK;
   XFH_REQUIRE(q && out && (a.K == 0 || (k && v)), "dot_product_attention: null tensor");
+  // bf16 with head dims <= 64, a batch-shared bias and a per-(batch entry, key) mask (the
+  // single-track and diffusion shapes) run on the triangle-attention kernel given a
+  // workspace of xfh_dot_product_attention_workspace_size bytes; the rest, or a call
+  // without workspace, on the general kernel.
+  if (workspace && mha_supported(a, dtype)) return mha(a, workspace, workspace_bytes, as_stream(stream));
   return attention(a, dtype, as_stream(stream));
 }
 
@@ -430,9 +433,12 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
     ga.out = static_cast<bf16 *>(p.attn);
     ga.osb = row_b * c;
     ga.ost = row_t * c;
-    ga.B = int(n); ga.H = int(heads); ga.N = int(n);
+    ga.ohs = dh;
+    ga.B = int(n); ga.H = int(heads); ga.Nq = int(n); ga.N = int(n);
     ga.Npad = int(npad);
     ga.Nblk = ga.Npad / 64;
+    ga.mbs = ga.Nblk;
+    ga.Dv = int(dh);
     XFH_TRY(grid_attention(ga, s));
     GridOutputArgs oa;
     oa.pair = pair; oa.attn = static_cast<const bf16 *>(p.attn);

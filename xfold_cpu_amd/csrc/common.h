@@ -50,8 +50,22 @@ class KernelTimer {
 };
 // Compute units of the current device (cached per device).
 int device_cu_count(int *cus);
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+
+// Bump allocator over a caller-provided workspace; 256-byte aligned slices.
+struct Carver {
+  char *base;
+  int64_t used = 0, cap;
+  Carver(void *b, int64_t c) : base(static_cast<char *>(b)), cap(c) {}
+  void *take(int64_t bytes) {
+    used = align_up(used, 256);
+    void *p = base ? base + used : nullptr;
+    used += bytes;
+    return p;
+  }
+};
 
 // ---------------------------------------------------------------- device helpers
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return static_cast<float>(v); }

@@ -35,6 +35,7 @@
 //     tile (a rank-1 product), blocks with no kept key are skipped.
 // Workgroups are numbered so that one XCD walks the row groups of one head, keeping that
 // head's bias in its L2.
+#include <string>
 #include <type_traits>
 
 #include "common.h"
@@ -44,10 +45,7 @@ namespace xfh {
 
 namespace {
 
-constexpr int GD = 32;               // head dim
 constexpr int GKB = 64;              // keys per block
-constexpr int K_ELEMS = GKB * GD;    // K tile of one row: [64 keys][32], 64 B per key
-constexpr int V_ELEMS = GD * GKB;    // V^T tile of one row: [32 d][64 keys], 128 B per d
 constexpr int MB_ZERO = 64;          // zeros read by the lanes that supply no mask value
 // Mask words of a row group are kept in registers (lane w holds word w of each row): a
 // global read inside the key loop would wait (vmcnt) for the block prefetch issued before it.
@@ -60,17 +58,32 @@ constexpr float kMaskedLogit = -1.0e30f;
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
-// Workgroup shape: R batch rows, W wavefronts, TQ tiles of 16 queries per wavefront.
-template <int R_, int W_, int TQ_> struct Shape {
-  static constexpr int R = R_, W = W_, TQ = TQ_;
+// Workgroup shape: R batch rows, W wavefronts, TQ tiles of 16 queries per wavefront, head
+// dim D (32 or 64; smaller heads are zero-padded).
+template <int R_, int W_, int TQ_, int D_> struct Shape {
+  static constexpr int R = R_, W = W_, TQ = TQ_, D = D_;
   static constexpr int Q = 16 * TQ * W;                     // queries per workgroup
   static constexpr int T = 64 * W;                          // threads
+  static constexpr int K_ELEMS = GKB * D;                   // K tile of one row: [64 keys][D]
+  static constexpr int V_ELEMS = D * GKB;                   // V^T tile of one row: [D][64 keys]
   static constexpr int STAGE = R * (K_ELEMS + V_ELEMS + GKB); // + one additive mask row per row
-  static constexpr int BLOCKS = 8 / W;                      // workgroups per CU (2 waves per SIMD)
+  static constexpr int KPIECES = D / 8, PIECES = 2 * KPIECES; // 1 KB direct loads per row
+  static constexpr int KPP = 512 / D;                       // keys per K piece
+  static constexpr int DT = D / 16;                         // output tiles (+ 1 denominator)
+  static constexpr int KS = D / 32;                         // k-steps of Q.K^T
+  static constexpr int BLOCKS = (8 / W) * (R == 1 ? 2 : 1); // workgroups per CU
+  static_assert(D == 32 || D == 64, "head dim 32 or 64");
   static_assert(W >= R, "wavefront r writes row r's mask row");
-  static_assert(8 % W == 0, "each wavefront loads 8 / W of the eight 1 KB pieces of a row");
+  static_assert(PIECES % W == 0, "each wavefront loads the same number of pieces of a row");
 };
-using GridShape = Shape<4, 4, 1>;
+using GridShape = Shape<4, 4, 1, 32>;
+
+// K slot swizzle: 16-byte slot s of key j holds chunk s ^ kswz(j), so that the 16 keys of an
+// MFMA operand read (one chunk each) hit distinct bank groups for 64-byte (D = 32) and
+// 128-byte (D = 64) rows.
+template <int D> __host__ __device__ constexpr int kswz(int key) {
+  return D == 32 ? (key >> 2) & 3 : (key >> 1) & 7;
+}
 
 __device__ __forceinline__ int64_t xcd_logical(int64_t physical, int64_t per_xcd) {
   return (physical % 8) * per_xcd + physical / 8;
@@ -108,7 +121,9 @@ __device__ __forceinline__ float max16(const f32x4 (&s)[4]) {
 
 template <class S>
 __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAttentionArgs a) {
-  constexpr int R = S::R, W = S::W, TQ = S::TQ, GQ = S::Q, GT = S::T, STAGE = S::STAGE;
+  constexpr int R = S::R, W = S::W, TQ = S::TQ, GQ = S::Q, STAGE = S::STAGE, D = S::D;
+  constexpr int K_ELEMS = S::K_ELEMS, V_ELEMS = S::V_ELEMS, DT = S::DT, KS = S::KS;
+  constexpr int PW = S::PIECES / W;                  // pieces of a row per wavefront
   __shared__ __attribute__((aligned(16))) bf16 lds[2 * STAGE + MB_ZERO];
   auto kbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + r * K_ELEMS; };
   auto vbuf = [&](int stage, int r) -> bf16 * { return lds + stage * STAGE + R * K_ELEMS + r * V_ELEMS; };
@@ -117,7 +132,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
   };
   bf16 *const mzero = lds + 2 * STAGE;
 
-  const int qblocks = (a.N + GQ - 1) / GQ;
+  const int qblocks = (a.Nq + GQ - 1) / GQ;
   const int rgroups = (a.B + R - 1) / R;
   const int64_t total = int64_t(qblocks) * rgroups * a.H;
   const int64_t logical = xcd_logical(blockIdx.x, (total + 7) / 8);
@@ -132,8 +147,8 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
   const int q0 = qblk * GQ + wave * 16 * TQ;
 
   // Per-(row, query tile) state.
-  bf16x8 qf[R][TQ];
-  f32x4 o[R][TQ][3];
+  bf16x8 qf[R][TQ][KS];
+  f32x4 o[R][TQ][DT + 1];
   float m[R][TQ];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
@@ -141,12 +156,15 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
     for (int tq = 0; tq < TQ; ++tq) {
       const int q = q0 + 16 * tq + col;
-      bf16x8 z = {};
-      qf[r][tq] = z;
-      if (b < a.B && q < a.N)
-        qf[r][tq] = *reinterpret_cast<const bf16x8 *>(a.q + ((int64_t(b) * a.H + h) * a.N + q) * GD + grp * 8);
 #pragma unroll
-      for (int t = 0; t < 3; ++t) o[r][tq][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ks = 0; ks < KS; ++ks) {
+        bf16x8 z = {};
+        qf[r][tq][ks] = z;
+        if (b < a.B && q < a.Nq)
+          qf[r][tq][ks] = *reinterpret_cast<const bf16x8 *>(a.q + ((int64_t(b) * a.H + h) * a.Nq + q) * D + ks * 32 + grp * 8);
+      }
+#pragma unroll
+      for (int t = 0; t <= DT; ++t) o[r][tq][t] = f32x4{0.f, 0.f, 0.f, 0.f};
       m[r][tq] = kInitialMax;
     }
   }
@@ -156,17 +174,20 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
   for (int r = 0; r < R; ++r) {
     const int b = rg * R + r;
-    wr[r] = b < a.B && lane < a.Nblk ? a.maskbits[int64_t(b) * a.Nblk + lane] : 0;
+    wr[r] = b < a.B && lane < a.Nblk ? a.maskbits[int64_t(b) * a.mbs + lane] : 0;
   }
 
 
-  // Swizzled LDS offsets of this lane's K fragment (key kt*16 + col, chunk grp) and V^T
-  // fragments (row t*16 + col, chunk 4c + grp); the mask fragment (key kt*16 + col in
-  // k-slot 0) is read by the grp 0 lanes, the others read zeros.
-  const int kslot = (grp ^ ((col >> 2) & 3)) * 8;
+  // Swizzled LDS offsets of this lane's K fragments (key kt*16 + col, chunk 4 ks + grp; the
+  // swizzle of key kt*16 + col depends on col only) and V^T fragments (row t*16 + col,
+  // chunk 4c + grp); the mask fragment (key kt*16 + col in k-slot 0) is read by the grp 0
+  // lanes, the others read zeros.
+  int kslot[KS];
+#pragma unroll
+  for (int ks = 0; ks < KS; ++ks) kslot[ks] = ((4 * ks + grp) ^ kswz<D>(col)) * 8;
   const int vslot[2] = {((0 + grp) ^ ((col >> 1) & 7)) * 8, ((4 + grp) ^ ((col >> 1) & 7)) * 8};
 
-  // A operand of the denominator MFMA: V^T row 32 = ones, rows 33..47 = zeros.
+  // A operand of the denominator MFMA: V^T row D = ones, rows D+1..D+15 = zeros.
   // B operand of the mask MFMA: k = 0 is one for every query, the other k are zero.
   bf16x8 ones_a, ones_b;
 #pragma unroll
@@ -177,25 +198,25 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 
   // One key block goes global -> LDS without passing through registers
   // (global_load_lds_dwordx4: lane i of a wavefront writes bytes [16i, 16i + 16) of a
-  // 1 KB LDS segment): per row, four 1 KB pieces of K and four of V^T, spread over the
+  // 1 KB LDS segment): per row, D/8 1 KB pieces of K and D/8 of V^T, spread over the
   // wavefronts. The 16-byte slots are XOR-swizzled so that the 16 lanes of an MFMA
   // operand read hit 16 distinct bank groups:
-  //   K:   slot s of key j holds its 8-element chunk s ^ ((j >> 2) & 3)
+  //   K:   slot s of key j holds its 8-element chunk s ^ kswz(j)
   //   V^T: slot s of row d holds its 8-element chunk s ^ ((d >> 1) & 7)
   // K and V^T are zero for keys >= N (their logits are masked). Each lane's source is a
   // per-(row, block) uniform base plus a per-lane byte offset fixed for the kernel.
   // From the first block that needs the mask on, wavefront r < R also turns row r's mask
   // word into the additive mask row (0 or -1e30), before the loads: an LDS store after
   // them would wait for them to land.
-  uint32_t piece_off[8 / W];                         // bytes, per piece of this wavefront
+  uint32_t piece_off[PW];                            // bytes, per piece of this wavefront
 #pragma unroll
-  for (int j = 0; j < 8 / W; ++j) {
-    const int piece = wave + j * W, i = piece & 3;
-    if (piece < 4) {
-      const int key = i * 16 + (lane >> 2), kchunk = (lane & 3) ^ ((lane >> 4) & 3);
-      piece_off[j] = uint32_t(key * GD + kchunk * 8) * 2;
-    } else {
-      const int d = i * 8 + (lane >> 3), vchunk = (lane & 7) ^ ((d >> 1) & 7);
+  for (int j = 0; j < PW; ++j) {
+    const int piece = wave + j * W;
+    if (piece < S::KPIECES) {                        // keys KPP*piece .., D/8 lanes per key
+      const int key = piece * S::KPP + lane / (D / 8), slot = lane % (D / 8);
+      piece_off[j] = uint32_t(key * D + (slot ^ kswz<D>(key)) * 8) * 2;
+    } else {                                         // V^T rows 8 (piece - KPIECES) ..
+      const int d = (piece - S::KPIECES) * 8 + (lane >> 3), vchunk = (lane & 7) ^ ((d >> 1) & 7);
       piece_off[j] = uint32_t(d * a.Npad + vchunk * 8) * 2;
     }
   }
@@ -221,13 +242,13 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       if (b >= a.B) continue;                        // absent row: its tiles are never read
       const int64_t bh = int64_t(b) * a.H + h;
 #pragma unroll
-      for (int j = 0; j < 8 / W; ++j) {
-        const int piece = wave + j * W;              // 0..3: K keys 16 i.., 4..7: V^T rows 8 i..
-        const int i = piece & 3;
-        const char *base = piece < 4
-            ? reinterpret_cast<const char *>(a.k + (bh * a.Npad + int64_t(kb) * GKB) * GD)
-            : reinterpret_cast<const char *>(a.vt + bh * GD * a.Npad + int64_t(kb) * GKB);
-        bf16 *dst = piece < 4 ? kbuf(stage, r) + i * 16 * GD : vbuf(stage, r) + i * 8 * GKB;
+      for (int j = 0; j < PW; ++j) {
+        const int piece = wave + j * W;
+        const bool kp = piece < S::KPIECES;
+        const char *base = kp
+            ? reinterpret_cast<const char *>(a.k + (bh * a.Npad + int64_t(kb) * GKB) * D)
+            : reinterpret_cast<const char *>(a.vt + bh * D * a.Npad + int64_t(kb) * GKB);
+        bf16 *dst = kp ? kbuf(stage, r) + piece * 512 : vbuf(stage, r) + (piece - S::KPIECES) * 512;
         __builtin_amdgcn_global_load_lds((global_void *)(base + piece_off[j]), (lds_void *)dst, 16, 0, 0);
       }
     }
@@ -246,7 +267,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
   for (int tq = 0; tq < TQ; ++tq) {
     const int q = q0 + 16 * tq + col;
-    bias_rows[tq] = a.bias + (int64_t(h) * a.N + (q < a.N ? q : a.N - 1)) * a.Npad;
+    bias_rows[tq] = a.bias + (int64_t(h) * a.Nq + (q < a.Nq ? q : a.Nq - 1)) * a.Npad;
   }
   f32x4 bias[TQ][4];
   auto load_bias = [&](int kb) {
@@ -262,9 +283,16 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
     const bf16 *kr = kbuf(cur, r);
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
-      const bf16x8 kf = *reinterpret_cast<const bf16x8 *>(kr + (kt * 16 + col) * GD + kslot);
+      bf16x8 kf[KS];
 #pragma unroll
-      for (int tq = 0; tq < TQ; ++tq) s[tq][kt] = mfma16(kf, qf[r][tq], bias[tq][kt]);
+      for (int ks = 0; ks < KS; ++ks)
+        kf[ks] = *reinterpret_cast<const bf16x8 *>(kr + (kt * 16 + col) * D + kslot[ks]);
+#pragma unroll
+      for (int tq = 0; tq < TQ; ++tq) {
+        s[tq][kt] = mfma16(kf[0], qf[r][tq][0], bias[tq][kt]);
+#pragma unroll
+        for (int ks = 1; ks < KS; ++ks) s[tq][kt] = mfma16(kf[ks], qf[r][tq][ks], s[tq][kt]);
+      }
     }
     if (masked) {
       const bf16 *mr = grp == 0 ? mbuf(cur, r) + col : mzero;
@@ -283,7 +311,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
     const float mn = vmax(m[r][tq], query_max(lane_max));
     const float alpha = __builtin_amdgcn_exp2f(m[r][tq] - mn);
 #pragma unroll
-    for (int t = 0; t < 3; ++t) o[r][tq][t] *= alpha;
+    for (int t = 0; t <= DT; ++t) o[r][tq][t] *= alpha;
     m[r][tq] = mn;
   };
   // P = exp2(S - m), then O^T += V^T P^T and l += 1^T P^T, both query tiles.
@@ -302,13 +330,13 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < DT; ++t) {
         const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vr + (t * 16 + col) * GKB + vslot[c]);
 #pragma unroll
         for (int tq = 0; tq < TQ; ++tq) o[r][tq][t] = mfma16(vf, pf[tq][c], o[r][tq][t]);
       }
 #pragma unroll
-      for (int tq = 0; tq < TQ; ++tq) o[r][tq][2] = mfma16(ones_a, pf[tq][c], o[r][tq][2]);
+      for (int tq = 0; tq < TQ; ++tq) o[r][tq][DT] = mfma16(ones_a, pf[tq][c], o[r][tq][DT]);
     }
   };
   // Row with every key masked: P = 1 on every key of the block. V^T is zero for keys
@@ -321,7 +349,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
     for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < DT; ++t) {
         const bf16x8 vf = *reinterpret_cast<const bf16x8 *>(vr + (t * 16 + col) * GKB + vslot[c]);
 #pragma unroll
         for (int tq = 0; tq < TQ; ++tq) o[r][tq][t] = mfma16(vf, ones, o[r][tq][t]);
@@ -422,38 +450,64 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 #pragma unroll
     for (int tq = 0; tq < TQ; ++tq) {
       const int q = q0 + 16 * tq + col;
-      const float l = __shfl(o[r][tq][2][0], col, 64);   // denominator sits in lane `col`, grp 0
-      if (b >= a.B || q >= a.N) continue;
+      const float l = __shfl(o[r][tq][DT][0], col, 64);  // denominator sits in lane `col`, grp 0
+      if (b >= a.B || q >= a.Nq) continue;
       const float inv = 1.0f / (all_masked[r] ? float(a.N) : l);
-      bf16 *dst = a.out + int64_t(b) * a.osb + int64_t(q) * a.ost + h * GD + grp * 4;
+      bf16 *dst = a.out + int64_t(b) * a.osb + int64_t(q) * a.ost + int64_t(h) * a.ohs + grp * 4;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < DT; ++t) {
+        const int d = t * 16 + grp * 4;
         bf16x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = bf16(o[r][tq][t][e] * inv);
-        *reinterpret_cast<bf16x4 *>(dst + t * 16) = v;
+        if (d + 4 <= a.Dv) {
+          *reinterpret_cast<bf16x4 *>(dst + t * 16) = v;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (d + e < a.Dv) dst[t * 16 + e] = v[e];
+        }
       }
     }
   }
 }
 
-}  // namespace
+int64_t grid_attention_pad_(int64_t n) { return align_up(n, GKB); }
 
-int64_t grid_attention_pad(int64_t n) { return align_up(n, GKB); }
-
-int64_t grid_attention_max_n() { return int64_t(kMaxKeyBlocks) * GKB; }
-
-int grid_attention(const GridAttentionArgs &a, hipStream_t s) {
-  if (a.B == 0 || a.N == 0) return XFH_OK;
-  if (a.Nblk > kMaxKeyBlocks) return fail(XFH_EUNSUPPORTED, "grid_attention: more than 4096 keys");
-  using S = GridShape;
-  const int64_t qblocks = ceil_div(a.N, S::Q), rgroups = ceil_div(a.B, S::R);
+template <class S> int launch(const GridAttentionArgs &a, const char *name, hipStream_t s) {
+  if (a.B == 0 || a.Nq == 0 || a.N == 0) return XFH_OK;
+  if (a.Nblk > kMaxKeyBlocks) return fail(XFH_EUNSUPPORTED, std::string(name) + ": more than 4096 keys");
+  const int64_t qblocks = ceil_div(a.Nq, S::Q), rgroups = ceil_div(a.B, S::R);
   const int64_t total = qblocks * rgroups * a.H;
   const int64_t grid = ceil_div(total, 8) * 8;
-  if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "grid_attention: problem too large");
-  KernelTimer timer("grid_attention", s);
+  if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, std::string(name) + ": problem too large");
+  KernelTimer timer(name, s);
   grid_attention_kernel<S><<<dim3(grid), S::T, 0, s>>>(a);
-  return check_launch("grid_attention");
+  return check_launch(name);
 }
+
+}  // namespace
+
+int grid_attention(const GridAttentionArgs &a, hipStream_t s) {
+  return launch<GridShape>(a, "grid_attention", s);
+}
+
+int mha_attention(const GridAttentionArgs &a, int d, hipStream_t s) {
+  // Rows (batch entries) per workgroup share the bias tile; a single row keeps more
+  // workgroups per CU instead.
+  if (d == 32) {
+    if (a.B == 1) return launch<Shape<1, 4, 1, 32>>(a, "mha_attention", s);
+    return launch<Shape<4, 4, 1, 32>>(a, "mha_attention", s);
+  }
+  if (d == 64) {
+    if (a.B == 1) return launch<Shape<1, 4, 1, 64>>(a, "mha_attention", s);
+    return launch<Shape<2, 4, 1, 64>>(a, "mha_attention", s);
+  }
+  return fail(XFH_EUNSUPPORTED, "mha_attention: head dim must be 32 or 64");
+}
+
+int64_t grid_attention_pad(int64_t n) { return grid_attention_pad_(n); }
+
+int64_t grid_attention_max_n() { return int64_t(kMaxKeyBlocks) * GKB; }
 
 }  // namespace xfh

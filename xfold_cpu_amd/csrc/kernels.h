@@ -47,15 +47,23 @@ struct AttentionArgs {
   float scale;
 };
 int attention(const AttentionArgs &a, int dtype, hipStream_t s);
+// dot_product_attention on the triangle-attention kernel (mha.hip).
+int64_t mha_workspace_size(const AttentionArgs &a);
+bool mha_supported(const AttentionArgs &a, int dtype);
+int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStream_t s);
 
 // Triangle (grid) attention, bf16, head dim 32 (grid_attention.hip).
+// Layouts (D = padded head dim, 32 or 64): q [B][H][Nq][D] pre-scaled by d^-0.5 * log2(e);
+// k [B][H][Npad][D] and v^T [B][H][D][Npad] zero beyond the N keys (v^T keys permuted in
+// runs of 32, see grid_project); bias [H][Nq][Npad] fp32 times log2(e), shared by all b.
 struct GridAttentionArgs {
   const bf16 *q, *k, *vt;
   const float *bias;
-  const uint64_t *maskbits;  // [B][Npad/64], see grid_prepare
+  const uint64_t *maskbits;  // word w of row b at maskbits[b*mbs + w] (mbs 0: one shared row)
   bf16 *out;
-  int64_t osb, ost;          // out element (b, t, h, d) at out[b*osb + t*ost + h*32 + d]
-  int B, H, N, Npad, Nblk;
+  int64_t osb, ost, ohs;     // out element (b, t, h, d) at out[b*osb + t*ost + h*ohs + d], d < Dv
+  int64_t mbs;
+  int B, H, Nq, N, Npad, Nblk, Dv;
 };
 // Fused grid-attention projection / output (grid_fused.hip), bf16, c = 128, 4 x 32 heads.
 struct GridProjectArgs {
@@ -88,6 +96,8 @@ int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb,
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s);
 int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 int64_t grid_attention_pad(int64_t n);
+// The same kernel for head dims 32 and 64 (d = 32 or 64) at the shapes of dot_product_attention.
+int mha_attention(const GridAttentionArgs &a, int d, hipStream_t s);
 int64_t grid_attention_max_n();
 int grid_attention(const GridAttentionArgs &a, hipStream_t s);
 

@@ -1,0 +1,221 @@
+// dot_product_attention (xfold/fastnn/attention.py:45-66) on the triangle-attention kernel
+// (grid_attention.hip): one preparation launch turns the caller's strided q, k, v, bias and
+// mask into that kernel's layouts, then the kernel runs at head dim 32 or 64.
+//
+// Preparation (one launch per part):
+//   0  q  [B][H][Nq][D]   = q * scale * log2(e), zero for d >= Dqk
+//   1  k  [B][H][Npad][D] = k, zero for keys >= N or d >= Dqk
+//   2  vt [B][H][D][Npad] = v^T, zero for keys >= N or d >= Dv; inside each run of 32 keys
+//      position 8g + j holds key 4g + j (j < 4) or 16 + 4g + j - 4 (j >= 4)
+//   3  bias [H][Nq][Npad] fp32 = bias * log2(e) (batch-shared), zero for keys >= N (part 5:
+//      the same from a bf16 view whose heads are innermost)
+//   4  mask words [Bm][Npad/64]: bit s of row b set iff key s < N is kept (Bm = B when the
+//      mask depends on the batch entry, else 1)
+#include "common.h"
+#include "kernels.h"
+
+namespace xfh {
+
+namespace {
+
+constexpr float kLog2eF = 1.4426950408889634f;
+
+struct MhaPrep {
+  AttentionArgs a;
+  int D;                      // padded head dim
+  int64_t npad, nblk, mask_rows;
+  bf16 *q, *k, *vt;
+  float *bias;
+  uint64_t *words;
+};
+
+template <typename T> __device__ __forceinline__ float ld(const void *p, int64_t i) {
+  return static_cast<float>(static_cast<const T *>(p)[i]);
+}
+
+__global__ void mha_prepare_kernel(MhaPrep p, int part) {
+  const AttentionArgs &a = p.a;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int D = p.D, dc = D / 8;            // 8-element chunks per row
+  switch (part) {
+    case 0: {                               // q: thread = (b, h, n, chunk)
+      const int64_t total = a.B * a.H * a.Q * dc;
+      if (idx >= total) return;
+      const int c = int(idx % dc);
+      const int64_t row = idx / dc, n = row % a.Q, bh = row / a.Q, h = bh % a.H, b = bh / a.H;
+      const bf16 *src = static_cast<const bf16 *>(a.q) + b * a.qs[0] + h * a.qs[1] + n * a.qs[2];
+      const float s = a.scale * kLog2eF;
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = c * 8 + e;
+        v[e] = bf16(d < a.D ? static_cast<float>(src[d]) * s : 0.f);
+      }
+      *reinterpret_cast<bf16x8 *>(p.q + row * D + c * 8) = v;
+      return;
+    }
+    case 1: {                               // k: thread = (b, h, key, chunk)
+      const int64_t total = a.B * a.H * p.npad * dc;
+      if (idx >= total) return;
+      const int c = int(idx % dc);
+      const int64_t row = idx / dc, key = row % p.npad, bh = row / p.npad, h = bh % a.H, b = bh / a.H;
+      const bf16 *src = static_cast<const bf16 *>(a.k) + b * a.ks[0] + h * a.ks[1] + key * a.ks[2];
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = c * 8 + e;
+        v[e] = (key < a.K && d < a.D) ? src[d] : bf16(0.f);
+      }
+      *reinterpret_cast<bf16x8 *>(p.k + row * D + c * 8) = v;
+      return;
+    }
+    case 2: {                               // v^T: thread = (b, h, 8-position group, d), d fastest
+      const int64_t groups = p.npad / 8;
+      const int64_t total = a.B * a.H * groups * D;
+      if (idx >= total) return;
+      const int d = int(idx % D);
+      const int64_t rest = idx / D, grp = rest % groups, bh = rest / groups, h = bh % a.H, b = bh / a.H;
+      const bf16 *src = static_cast<const bf16 *>(a.v) + b * a.vs[0] + h * a.vs[1] + d;
+      bf16x8 v;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int64_t pos = grp * 8 + e, run = pos & ~int64_t(31);
+        const int w = int(pos & 31), g = w >> 3, j = w & 7;
+        const int64_t key = run + (j < 4 ? 4 * g + j : 16 + 4 * g + j - 4);
+        v[e] = (key < a.K && d < a.Dv) ? src[key * a.vs[2]] : bf16(0.f);
+      }
+      *reinterpret_cast<bf16x8 *>(p.vt + (bh * D + d) * p.npad + grp * 8) = v;
+      return;
+    }
+    case 3: {                               // bias, key-minor view: thread = (h, q, 4 keys)
+      const int64_t quads = p.npad / 4;
+      const int64_t total = a.H * a.Q * quads;
+      if (idx >= total) return;
+      const int64_t kq = idx % quads, row = idx / quads, n = row % a.Q, h = row / a.Q;
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int64_t key = kq * 4 + e;
+        float x = 0.f;
+        if (key < a.K && a.bias) {
+          const int64_t off = h * a.bs[1] + n * a.bs[2] + key * a.bs[3];
+          x = (a.bias_dtype == XFH_F32 ? ld<float>(a.bias, off) : ld<bf16>(a.bias, off)) * kLog2eF;
+        }
+        v[e] = x;
+      }
+      *reinterpret_cast<float4 *>(p.bias + row * p.npad + kq * 4) = make_float4(v[0], v[1], v[2], v[3]);
+      return;
+    }
+    case 5: {                               // bias, bf16 head-minor view (heads contiguous, H % 8
+                                            // == 0, 16-byte aligned): thread = (q, key)
+      const int64_t total = a.Q * p.npad;
+      if (idx >= total) return;
+      const int64_t key = idx % p.npad, n = idx / p.npad;
+      const bf16 *src = static_cast<const bf16 *>(a.bias) + n * a.bs[2] + key * a.bs[3];
+      float *dst = p.bias + n * p.npad + key;
+      for (int64_t h0 = 0; h0 < a.H; h0 += 8) {
+        bf16x8 v = {};
+        if (key < a.K) v = *reinterpret_cast<const bf16x8 *>(src + h0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dst[(h0 + e) * a.Q * p.npad] = static_cast<float>(v[e]) * kLog2eF;
+      }
+      return;
+    }
+    default: {                              // mask words: one wavefront per word
+      const int64_t word = idx >> 6;
+      if (word >= p.mask_rows * p.nblk) return;
+      const int64_t b = word / p.nblk, w = word % p.nblk;
+      const int64_t key = w * 64 + (threadIdx.x & 63);
+      const bool keep = key < a.K && (!a.mask || load_any(a.mask, a.mask_dtype, b * a.ms[0] + key * a.ms[3]) != 0.f);
+      const uint64_t ballot = __ballot(keep);
+      if ((threadIdx.x & 63) == 0) p.words[word] = ballot;
+      return;
+    }
+  }
+}
+
+int padded_dim(int64_t d) { return d <= 32 ? 32 : d <= 64 ? 64 : 0; }
+
+struct MhaPlan {
+  int D;
+  int64_t npad, nblk, mask_rows;
+  int64_t q_bytes, k_bytes, v_bytes, bias_bytes, word_bytes;
+  int64_t total() const { return q_bytes + k_bytes + v_bytes + bias_bytes + word_bytes + 5 * 256; }
+};
+
+MhaPlan plan(int64_t B, int64_t H, int64_t Q, int64_t K, int64_t D, int64_t Dv, bool mask_per_row) {
+  MhaPlan p;
+  p.D = padded_dim(D > Dv ? D : Dv);
+  p.npad = align_up(K, 64);
+  p.nblk = p.npad / 64;
+  p.mask_rows = mask_per_row ? B : 1;
+  p.q_bytes = B * H * Q * p.D * 2;
+  p.k_bytes = B * H * p.npad * p.D * 2;
+  p.v_bytes = B * H * p.D * p.npad * 2;
+  p.bias_bytes = H * Q * p.npad * 4;
+  p.word_bytes = p.mask_rows * p.nblk * 8;
+  return p;
+}
+
+}  // namespace
+
+int64_t mha_workspace_size(const AttentionArgs &a) {
+  if (padded_dim(a.D > a.Dv ? a.D : a.Dv) == 0) return 0;
+  return plan(a.B, a.H, a.Q, a.K, a.D, a.Dv, true).total();
+}
+
+bool mha_supported(const AttentionArgs &a, int dtype) {
+  return dtype == XFH_BF16 && a.out_dtype == XFH_BF16 && padded_dim(a.D > a.Dv ? a.D : a.Dv) != 0 &&
+         a.K > 0 && align_up(a.K, 64) <= grid_attention_max_n() &&
+         (!a.bias || a.B == 1 || a.bs[0] == 0) &&           // bias shared by the batch entries
+         (!a.mask || (a.ms[1] == 0 && a.ms[2] == 0)) &&      // mask per (batch entry, key)
+         a.os[1] % 4 == 0 && a.os[2] % 4 == 0 && a.os[0] % 4 == 0 &&
+         reinterpret_cast<uintptr_t>(a.o) % 8 == 0;
+}
+
+int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStream_t s) {
+  const bool per_row = a.mask && a.B > 1 && a.ms[0] != 0;
+  const MhaPlan pl = plan(a.B, a.H, a.Q, a.K, a.D, a.Dv, per_row);
+  if (!workspace || pl.total() > workspace_bytes)
+    return fail(XFH_EWORKSPACE, "dot_product_attention: workspace too small (need " +
+                                    std::to_string(pl.total()) + " bytes)");
+  Carver cv(workspace, workspace_bytes);
+  MhaPrep p;
+  p.a = a;
+  p.D = pl.D;
+  p.npad = pl.npad;
+  p.nblk = pl.nblk;
+  p.mask_rows = pl.mask_rows;
+  p.q = static_cast<bf16 *>(cv.take(pl.q_bytes));
+  p.k = static_cast<bf16 *>(cv.take(pl.k_bytes));
+  p.vt = static_cast<bf16 *>(cv.take(pl.v_bytes));
+  p.bias = static_cast<float *>(cv.take(pl.bias_bytes));
+  p.words = static_cast<uint64_t *>(cv.take(pl.word_bytes));
+  const int dc = pl.D / 8;
+  const int64_t work[5] = {a.B * a.H * a.Q * dc, a.B * a.H * pl.npad * dc, a.B * a.H * (pl.npad / 8) * pl.D,
+                           a.H * a.Q * (pl.npad / 4), pl.mask_rows * pl.nblk * 64};
+  // Bias views with the heads innermost (the diffusion transformer's rearranged pair logits)
+  // are read a whole head vector per thread.
+  const bool head_minor = a.bias && a.bias_dtype == XFH_BF16 && a.bs[1] == 1 && a.H % 8 == 0 &&
+                          a.bs[2] % 8 == 0 && a.bs[3] % 8 == 0 &&
+                          reinterpret_cast<uintptr_t>(a.bias) % 16 == 0;
+  for (int part = 0; part < 5; ++part) {
+    const int64_t n_work = part == 3 && head_minor ? a.Q * pl.npad : work[part];
+    const int64_t blocks = ceil_div(n_work, 256);
+    if (blocks == 0) continue;
+    if (blocks > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "dot_product_attention: problem too large");
+    mha_prepare_kernel<<<dim3(unsigned(blocks)), 256, 0, s>>>(p, part == 3 && head_minor ? 5 : part);
+  }
+  XFH_TRY(check_launch("mha_prepare"));
+
+  GridAttentionArgs ga;
+  ga.q = p.q; ga.k = p.k; ga.vt = p.vt; ga.bias = p.bias; ga.maskbits = p.words;
+  ga.out = static_cast<bf16 *>(a.o);
+  ga.osb = a.os[0]; ga.ost = a.os[2]; ga.ohs = a.os[1];
+  ga.mbs = per_row ? pl.nblk : 0;
+  ga.B = int(a.B); ga.H = int(a.H); ga.Nq = int(a.Q); ga.N = int(a.K);
+  ga.Npad = int(pl.npad); ga.Nblk = int(pl.nblk); ga.Dv = int(a.Dv);
+  return mha_attention(ga, pl.D, s);
+}
+
+}  // namespace xfh

@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, BF16, BOOL = 0, 1, 2
 EPI_STORE, EPI_MUL_SIGMOID_AUX, EPI_SIGMOID_MUL_AUX, EPI_ACCUMULATE, EPI_MUL_SIGMOID_AUX_ACCUMULATE = range(5)
@@ -49,7 +49,8 @@ SIGNATURES = {
     "xfh_glu_packed_rows": (_i64, [_i64]),
     "xfh_glu_pack_weight": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "xfh_gated_linear_unit": (_i, [_p, _p, _i64, _i64, _i64, _i, _p, _i, _p]),
-    "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _pi64, _pi64, _f, _p]),
+    "xfh_dot_product_attention_workspace_size": (_i64, [_pi64, _i]),
+    "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _pi64, _pi64, _f, _p, _i64, _p]),
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
     "xfh_triangle_multiplication": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,
                                          _f, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),

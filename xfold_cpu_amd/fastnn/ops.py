@@ -159,8 +159,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
         *mask_strides, *bias_strides)
+    lib = nh.load_library()
+    ws = nh.workspace(lib.xfh_dot_product_attention_workspace_size(shape, nh.dtype_code(dtype)), q.device)
     nh.call("xfh_dot_product_attention", nh.ptr(q), nh.ptr(k), nh.ptr(v), nh.dtype_code(dtype),
             nh.ptr(mask_t), mask_code, nh.ptr(bias_t), bias_code, nh.ptr(out), nh.dtype_code(out.dtype),
             shape, strides,
-            float(D ** -0.5 if scale is None else scale), nh.stream_of(q.device))
+            float(D ** -0.5 if scale is None else scale), nh.ptr(ws), ws.numel(), nh.stream_of(q.device))
     return out
