@@ -262,6 +262,28 @@ def test_triangle_multiplication(device, n, outgoing, bf16):
                  (pair.to(device), mask.to(device)), bf16, "trimul", bf16_floor.triangle_multiplication)
 
 
+# n = 520: enough 32-position units (520 x 17) for the 32-position projection path on a
+# 256-CU device; the smaller sizes take the 16-position path.
+@pytest.mark.parametrize("n,mask_dtype", [(33, torch.float32), (96, torch.bfloat16), (45, torch.bool),
+                                          (520, torch.float32)])
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_triangle_multiplication_mask_values(device, n, mask_dtype, outgoing):
+    """Fractional (float, bf16) and boolean masks, asymmetric, on sizes with and without pad
+    columns in the contraction operands: the mask scales every projected channel of its
+    position, in the orientation the module reads it."""
+    announce("trimul mask", n, mask_dtype, outgoing)
+    ref, hip = pair_of("TriangleMultiplication", dict(c_pair=128, _outgoing=outgoing), seed=n + 7)
+    g = torch.Generator().manual_seed(n)
+    pair = torch.randn(n, n, 128, generator=g).bfloat16()
+    if mask_dtype == torch.bool:
+        mask = torch.rand(n, n, generator=g) > 0.3
+    else:
+        mask = torch.rand(n, n, generator=g).to(mask_dtype)
+    mask[0, 1] = 0                       # asymmetric
+    check_module(ref, hip, hnn.triangle_multiplication_hip, (pair.float(), mask.float()),
+                 (pair.to(device), mask.to(device)), True, "trimul mask")
+
+
 @pytest.mark.parametrize("n", [5, 37, 70])
 @pytest.mark.parametrize("transpose", [False, True])
 @pytest.mark.parametrize("bf16", [False, True])

@@ -15,7 +15,7 @@
 //   bias [H][N][Npad] fp32, pre-multiplied by log2(e)
 //   maskbits [B][Npad/64] uint64: bit s%64 of word s/64 set iff key s < N is kept
 //
-// One workgroup = one head, 128 queries (8 wavefronts x 16) and R = 4 batch rows; keys go
+// One workgroup = one head, 64 queries (4 wavefronts x 16) and R = 4 batch rows; keys go
 // in blocks of 64 through a double-buffered LDS stage filled by direct global->LDS loads
 // (one barrier per block). Per block:
 //   - the bias tile [16 q x 64 keys] is loaded once (prefetched a block ahead) and is the
@@ -85,7 +85,7 @@ template <int D> __host__ __device__ constexpr int kswz(int key) {
   return D == 32 ? (key >> 2) & 3 : (key >> 1) & 7;
 }
 
-__device__ __forceinline__ int64_t xcd_logical(int64_t physical, int64_t per_xcd) {
+__device__ __forceinline__ uint32_t xcd_logical(uint32_t physical, uint32_t per_xcd) {
   return (physical % 8) * per_xcd + physical / 8;
 }
 
@@ -132,14 +132,16 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
   };
   bf16 *const mzero = lds + 2 * STAGE;
 
-  const int qblocks = (a.Nq + GQ - 1) / GQ;
-  const int rgroups = (a.B + R - 1) / R;
-  const int64_t total = int64_t(qblocks) * rgroups * a.H;
-  const int64_t logical = xcd_logical(blockIdx.x, (total + 7) / 8);
+  // 32-bit work decomposition (the launcher keeps the grid below 2^31).
+  const uint32_t qblocks = (a.Nq + GQ - 1) / GQ;
+  const uint32_t rgroups = (a.B + R - 1) / R;
+  const uint32_t total = qblocks * rgroups * uint32_t(a.H);
+  const uint32_t logical = xcd_logical(blockIdx.x, (total + 7) / 8);
   if (logical >= total) return;
-  const int qblk = int(logical % qblocks);
-  const int rg = int((logical / qblocks) % rgroups);
-  const int h = int(logical / (int64_t(qblocks) * rgroups));
+  const uint32_t rest = logical / qblocks;
+  const int qblk = int(logical - rest * qblocks);
+  const int h = int(rest / rgroups);
+  const int rg = int(rest - uint32_t(h) * rgroups);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;

@@ -8,10 +8,9 @@
 //       times sigmoid(gating_linear(LN_in(z))) (recomputed from z, which this kernel reads
 //       anyway for the residual) -> z += update (or update stored).
 //
-// trimul_project is a row-panel kernel (panel.h, 128 pair positions per workgroup, so each
-// channel's row of the operand layout is written 256 bytes at a time); trimul_output works
-// on register-resident rows (rowstep.h).
+// Both work on register-resident rows (rowstep.h) with their weights resident in LDS.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -24,90 +23,111 @@ namespace {
 
 using namespace panel;
 
-constexpr int SPITCH = ROWS + 8;     // staging row pitch (bf16): [channel][position]
+// trimul_project, one wavefront per unit of 16 RT positions (x, y0 .. y0 + 16 RT - 1) at a
+// time (y0 a multiple of 16 RT, y up to ld: the pad columns n <= y < ld come out as zeros), the
+// projection and gate weights resident in LDS (rowstep.h layout), the next unit's rows
+// loaded while this one is computed, no barriers after the weights are in:
+//   x      = bf16(LN_in(z))                    RT K-layout sets (row tiles rt < RT)
+//   p, g   = x . Wproj^T, x . Wgate^T          rows = positions, 16 channels per tile
+//   out    = p * sigmoid(g) * mask             channel 2k -> a_k, 2k + 1 -> b_k
+// With RT = 2, row m of row tile rt is position y0 + 8 (m / 4) + 4 rt + m % 4, so that the
+// lane that holds channel c of rows 4 g .. 4 g + 3 in both tiles has positions y0 + 8 g .. + 7
+// of c: one 16-byte store into the channel-major operand row. RT = 1 (row m = position
+// y0 + m, 8-byte stores) halves the unit for grids too small to give every wavefront
+// several 32-position units.
+constexpr int PROJ = 2 * K;          // projection (and gate) output channels
 
-template <typename TIN>
-__global__ __launch_bounds__(256, 2) void trimul_project_kernel(TriProjectArgs a) {
-  __shared__ bf16 lds_a[A_ELEMS];                 // A tile, later two B buffers
-  __shared__ bf16 stage[32 * SPITCH];             // 32 channels x 128 positions
-  __shared__ float mval[ROWS];
-  auto bbuf = [&](int i) -> bf16 * { return lds_a + (i & 1) * B_ELEMS; };
+template <typename TIN, int RT>
+__global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a) {
+  constexpr int UP = 16 * RT;                       // positions per unit
+  // Position offset (in the unit) of row m of row tile rt, and of output element i < 4 RT
+  // of a lane in channel-tile group g.
+  auto row_y = [](int rt, int m) { return RT == 2 ? 8 * (m >> 2) + 4 * rt + (m & 3) : m; };
+  __shared__ __attribute__((aligned(16))) bf16 w_proj[PROJ * K];
+  __shared__ __attribute__((aligned(16))) bf16 w_gate[PROJ * K];
+  __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
+  rowstep::load_weight(a.w_proj, w_proj, false, PROJ);
+  rowstep::load_weight(a.w_gate, w_gate, false, PROJ);
+  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
+  __syncthreads();
 
-  const int n = a.n;
-  const int ppx = (n + ROWS - 1) / ROWS;          // panels per grid line
-  const int x = blockIdx.x / ppx, y0 = (blockIdx.x % ppx) * ROWS;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
+  const int n = a.n, cpr = a.ld / UP;               // units per grid line
+  const int units = n * cpr;                        // < 2^31 (n * ld fits in 32 bits)
+  const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+  const int waves = int(gridDim.x) * int(blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
-  // Pair position of panel row r: (x, y) outgoing, (y, x) incoming.
-  auto pos_of = [&](int r) -> int64_t {
-    const int64_t y = y0 + r;
-    return a.outgoing ? int64_t(x) * n + y : y * n + x;
-  };
-  if (tid < ROWS) {
-    float m = 0.f;
-    if (y0 + tid < n) m = a.mask ? load_any(a.mask, a.mask_dtype, pos_of(tid)) : 1.f;
-    mval[tid] = m;
-  }
-  ln_panel<TIN>([&](int r) -> const TIN * { return (y0 + r < n) ? z + pos_of(r) * K : nullptr; },
-                a.ln_w, a.ln_b, a.eps, lds_a);
-  __syncthreads();
-  AFrags af;
-  load_a_frags(lds_a, wm, af);
-  // Weight row r of chunk j = r / 64 (64 rows): projection rows 32j..32j+15, gate rows
-  // 32j..32j+15, projection rows 32j+16..32j+31, gate rows 32j+16..32j+31.
-  auto wrow = [&](int r) -> const bf16 * {
-    const int j = r >> 6, s4 = (r >> 4) & 3, i = r & 15;
-    return ((s4 & 1) ? a.w_gate : a.w_proj) + (32 * j + (s4 >= 2 ? 16 : 0) + i) * K;
-  };
-  BStage st;
-  const int nout = 4 * K;                          // projection + gate, 2c each
-  fetch_rows(wrow, 0, st);
-  __syncthreads();                                 // A tile consumed; reuse as B buffers
-  stash_b(st, bbuf(0));
-  __syncthreads();
-
-  bf16 *left = a.left, *right = a.right;
   const int64_t plane = int64_t(n) * a.ld;
-  const int chunks = nout / CHUNK;
-  for (int j = 0; j < chunks; ++j) {
-    if (j + 1 < chunks) fetch_rows(wrow, (j + 1) * CHUNK, st);
-    f32x4 acc[4][2];
-    zero(acc);
-    mma_chunk(af, bbuf(j), wn, acc);
-    // Sub-tile 0 = projection, 1 = gate of projection channel 32j + 16*wn + col.
+  // Pair position of grid-line entry (x, y): (x, y) outgoing, (y, x) incoming.
+  auto pos_of = [&](int x, int y) -> int64_t { return a.outgoing ? int64_t(x) * n + y : int64_t(y) * n + x; };
+
+  struct Unit {
+    rowstep::Raw4<TIN> z[RT][8];                    // K-layout rows of the row tiles
+    float mrow[RT];                                 // mask of those rows (0 for y >= n)
+  };
+  auto fetch = [&](int u, Unit &w) {
+    const int x = u / cpr, y0 = (u - x * cpr) * UP;
 #pragma unroll
-    for (int mt = 0; mt < 4; ++mt) {
-      const int r0 = wm * 64 + mt * 16 + grp * 4;
-      bf16x4 v;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = bf16(acc[mt][0][e] * sigmoidf_(acc[mt][1][e]) * mval[r0 + e]);
-      *reinterpret_cast<bf16x4 *>(&stage[(wn * 16 + col) * SPITCH + r0]) = v;
+    for (int rt = 0; rt < RT; ++rt) {
+      const int y = y0 + row_y(rt, m);
+      const int64_t pos = pos_of(x, y < n ? y : n - 1);
+      rowstep::load_k<TIN>(z + pos * K, w.z[rt]);
+      w.mrow[rt] = y >= n ? 0.f : a.mask ? load_any(a.mask, a.mask_dtype, pos) : 1.f;
     }
-    __syncthreads();
-    // 32 projection channels x 128 positions -> left/right[k][x][y0 + ...], with zeros in
-    // the pad columns y in [n, ld) (ld is a multiple of 32, so a chunk of 8 is either all
-    // below ld or all above).
+  };
+  int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
+  Unit cur;
+  if (u < units) fetch(u, cur);
+  for (; u < units; u += waves) {
+    Unit next;
+    if (u + waves < units) fetch(u + waves, next);
+    bf16x8 xa[RT][4];
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = tid + i * 256;
-      const int ch = idx >> 4, yc = (idx & 15) * 8;
-      const int y = y0 + yc;
-      if (y >= a.ld) continue;
-      const int p = j * 32 + ch;                    // projection channel
-      const bool is_a = (p & 1) == 0;
-      bf16 *dst = ((a.outgoing != 0) == is_a ? left : right) + int64_t(p >> 1) * plane +
-                  int64_t(x) * a.ld + y;
-      bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[ch * SPITCH + yc]);
-      if (y + 8 > n) {
+    for (int rt = 0; rt < RT; ++rt) {
+      float v[32];
+      rowstep::k_to_float(cur.z[rt], v);
+      rowstep::ln_k(v, lnw, lnb, a.eps, xa[rt]);
+    }
+    // Mask of output rows 4 g + e of tile rt: held by A-row lane 4 g + e.
+    float mk[4 * RT];
 #pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (y + e >= n) v[e] = bf16(0.0f);
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) mk[4 * rt + e] = __shfl(cur.mrow[rt], 4 * g + e, 64);
+    const int x = u / cpr, y0 = (u - x * cpr) * UP;
+    const int y_lane = y0 + 4 * RT * g;             // positions y_lane .. + 4 RT - 1
+    const int64_t row_off = int64_t(x) * a.ld + y_lane;
+    const bool pad = y0 + UP > n;
+#pragma unroll 1
+    for (int t = 0; t < PROJ / 16; ++t) {
+      f32x4 ap[RT], ag[RT];
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) ap[rt] = ag[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 wp = rowstep::weight_frag(w_proj, t, ks), wg = rowstep::weight_frag(w_gate, t, ks);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+          ap[rt] = mfma16(xa[rt][ks], wp, ap[rt]);
+          ag[rt] = mfma16(xa[rt][ks], wg, ag[rt]);
+        }
       }
-      *reinterpret_cast<bf16x8 *>(dst) = v;
+      using Out = std::conditional_t<RT == 2, bf16x8, bf16x4>;
+      Out o;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[4 * rt + e] = bf16(ap[rt][e] * sigmoidf_(ag[rt][e]) * mk[4 * rt + e]);
+      if (pad) {
+#pragma unroll
+        for (int e = 0; e < 4 * RT; ++e)
+          if (y_lane + e >= n) o[e] = bf16(0.0f);
+      }
+      const int p = 16 * t + m;                     // projection channel
+      const bool is_a = (p & 1) == 0;
+      bf16 *dst = ((a.outgoing != 0) == is_a ? a.left : a.right) + int64_t(p >> 1) * plane + row_off;
+      *reinterpret_cast<Out *>(dst) = o;
     }
-    if (j + 1 < chunks) stash_b(st, bbuf(j + 1));
-    __syncthreads();
+    cur = next;
   }
 }
 
@@ -260,12 +280,23 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
 }  // namespace
 
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
-  const int64_t panels = int64_t(a.n) * ceil_div(a.n, ROWS);
+  if (a.ld % 32 != 0 || a.ld < a.n) return fail(XFH_EINVAL, "trimul_project: ld must be a multiple of 32, >= n");
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  // 32-position units unless that leaves fewer than four per wavefront (the last round of
+  // units would then run on a fraction of the wavefronts).
+  const int64_t units32 = int64_t(a.n) * (a.ld / 32);
+  const bool wide = units32 >= int64_t(cus) * 8 * 4;
+  const int64_t units = wide ? units32 : 2 * units32;
+  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
   KernelTimer timer("trimul_project", s);
-  if (pair_dtype == XFH_BF16)
-    trimul_project_kernel<bf16><<<dim3(panels), 256, 0, s>>>(a);
-  else
-    trimul_project_kernel<float><<<dim3(panels), 256, 0, s>>>(a);
+  if (pair_dtype == XFH_BF16) {
+    if (wide) trimul_project_kernel<bf16, 2><<<grid, 512, 0, s>>>(a);
+    else trimul_project_kernel<bf16, 1><<<grid, 512, 0, s>>>(a);
+  } else {
+    if (wide) trimul_project_kernel<float, 2><<<grid, 512, 0, s>>>(a);
+    else trimul_project_kernel<float, 1><<<grid, 512, 0, s>>>(a);
+  }
   return check_launch("trimul_project");
 }
 
