@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 2
+#define XFH_ABI_VERSION 3
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -81,6 +81,17 @@ int xfh_linear(const void *x, int64_t ldx, const void *w, const float *bias,
                void *y, int64_t ldy, int y_dtype,
                int epilogue, const void *aux, int64_t ldaux, int64_t aux_rows,
                void *stream);
+
+/* Batched plain linear: for b < batch, y[b] = x[b] @ w[b]^T (+ bias[b]) with
+ * x[b] = x + b*sx ([m, k] rows of ldx; sx = 0 shares one input), w[b] = w + b*sw ([n, k]),
+ * bias[b] = bias + b*sbias (fp32, may be null), y[b] = y + b*sy ([m, n] rows of ldy).
+ * No counterpart in the reference, which runs each block's conditioning linears
+ * (AdaptiveLayerNorm and AdaLNZero, xfold/nn/diffusion_transformer.py:59-62, 93) as
+ * separate nn.Linear calls; the hip DiffusionTransformer runs all of its blocks' ones as
+ * one launch per input. */
+int xfh_linear_batched(const void *x, int64_t ldx, int64_t sx, const void *w, int64_t sw,
+                       const float *bias, int64_t sbias, int64_t m, int64_t k, int64_t n, int64_t batch,
+                       int dtype, void *y, int64_t ldy, int64_t sy, int y_dtype, void *stream);
 
 /* Rows of the packed GLU weight for f output features (gate and value interleaved in
  * groups of 16 features, zero rows pad f up to a multiple of 16). */

@@ -46,6 +46,8 @@ def test_invalid_arguments_fail_before_any_launch():
         nh.call("xfh_linear", None, 4, None, None, 4, 4, 4, 0, None, 4, 0, 99, None, 4, 0, None)
     with pytest.raises(ValueError, match="aux"):
         nh.call("xfh_linear", None, 4, None, None, 4, 4, 4, 0, None, 4, 0, nh.EPI_MUL_SIGMOID_AUX, None, 4, 0, None)
+    with pytest.raises(ValueError, match="overlap"):
+        nh.call("xfh_linear_batched", None, 4, 0, None, 16, None, 0, 4, 4, 4, 2, 0, None, 4, 8, 0, None)
     with pytest.raises(ValueError, match="head dim"):
         nh.call("xfh_grid_self_attention", None, 0, None, 2, 8, 512, 4, 0, None, None, 1e-5,
                 None, None, None, None, None, None, 0, None, 0, 0, None, 0, None)
@@ -78,6 +80,7 @@ def test_empty_inputs_are_no_ops():
     lib = nh.load_library()
     assert lib.xfh_layer_norm(None, 0, 0, 128, None, None, 1e-5, None, 0, None) == 0
     assert lib.xfh_linear(None, 4, None, None, 0, 4, 4, 1, None, 4, 1, 0, None, 4, 0, None) == 0
+    assert lib.xfh_linear_batched(None, 4, 0, None, 16, None, 0, 4, 4, 4, 0, 1, None, 4, 16, 1, None) == 0
 
 
 def test_config_defaults_to_hip_and_rejects_other_backends():

@@ -124,6 +124,29 @@ def test_linear_epilogues(device, m, k, n, dtype, epi):
         assert_parity_bf16(out32, want, "linear bf16 compute, fp32 out")
 
 
+@pytest.mark.parametrize("m,k,n,nb", [(77, 384, 768, 6), (5, 64, 40, 3), (300, 96, 130, 2)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shared", [True, False])
+@pytest.mark.parametrize("with_bias", [True, False])
+def test_linear_batched(device, m, k, n, nb, dtype, shared, with_bias):
+    """One launch over B weight matrices (and biases), with one shared input or B inputs."""
+    announce("linear_batched", m, k, n, nb, dtype, shared, with_bias)
+    torch.manual_seed(m + n + nb)
+    x = torch.randn(m, k) if shared else torch.randn(nb, m, k)
+    x = x.to(dtype)
+    w = (torch.randn(nb, n, k) / math.sqrt(k)).to(dtype)
+    bias = torch.randn(nb, n) if with_bias else None
+    want = torch.einsum("mk,bnk->bmn" if shared else "bmk,bnk->bmn", x.float(), w.float())
+    if with_bias:
+        want = want + bias[:, None, :]
+    got = ops.linear_batched(x.to(device), w.to(device), None if bias is None else bias.to(device), dtype)
+    assert got.shape == (nb, m, n) and got.dtype == dtype
+    if dtype == torch.float32:
+        assert_parity(got, want, TOL_FP32, "linear_batched")
+    else:
+        assert_parity_bf16(got, want, "linear_batched")
+
+
 def test_linear_aux_rows_broadcast(device):
     torch.manual_seed(2)
     x, w, aux = torch.randn(3, 10, 64), torch.randn(32, 64) / 8, torch.randn(10, 32)

@@ -244,6 +244,25 @@ int xfh_linear(const void *x, int64_t ldx, const void *w, const float *bias, int
   return gemm_nt(g, 1, dtype, y_dtype, false, as_stream(stream));
 }
 
+int xfh_linear_batched(const void *x, int64_t ldx, int64_t sx, const void *w, int64_t sw,
+                       const float *bias, int64_t sbias, int64_t m, int64_t k, int64_t n, int64_t batch,
+                       int dtype, void *y, int64_t ldy, int64_t sy, int y_dtype, void *stream) {
+  XFH_REQUIRE(m >= 0 && k >= 0 && n >= 0 && batch >= 0, "linear_batched: negative size");
+  XFH_REQUIRE(m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && k < (int64_t(1) << 31),
+              "linear_batched: sizes must fit in 32 bits");
+  XFH_REQUIRE(batch <= 65535, "linear_batched: at most 65535 batch entries");
+  XFH_REQUIRE(float_dtype(dtype) && float_dtype(y_dtype), "linear_batched: dtypes must be f32/bf16");
+  XFH_REQUIRE(ldx >= k && ldy >= n && sx >= 0 && sw >= 0 && sbias >= 0 && sy >= 0,
+              "linear_batched: leading dims or batch strides invalid");
+  XFH_REQUIRE(batch <= 1 || sy >= m * ldy, "linear_batched: outputs of batch entries overlap");
+  if (m == 0 || n == 0 || batch == 0) return XFH_OK;
+  XFH_REQUIRE(x && w && y, "linear_batched: null tensor");
+  GemmArgs g = gemm_args(x, ldx, w, k, y, ldy, m, n, k);
+  g.sA = sx; g.sB = sw; g.sC = sy;
+  g.bias = bias; g.sBias = bias ? sbias : 0;
+  return gemm_nt(g, batch, dtype, y_dtype, false, as_stream(stream));
+}
+
 int64_t xfh_glu_packed_rows(int64_t f) { return 2 * align_up(f, 16); }
 
 int xfh_glu_pack_weight(const void *w, int64_t f, int64_t k, int dtype, void *packed, void *stream) {

@@ -158,7 +158,7 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
   for (int j = 0; j < 4; ++j) {
     const int n = n0 + wn * 64 + j * 16 + col_lane;
     if (n >= p.N) continue;
-    const float bias = p.bias ? p.bias[n] : 0.f;
+    const float bias = p.bias ? p.bias[batch * p.sBias + n] : 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll

@@ -173,7 +173,7 @@ __global__ __launch_bounds__(256, 2) void gemm_ring_kernel(GemmArgs p) {
     float bias[4] = {0.f, 0.f, 0.f, 0.f};
     if (p.bias)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bias[e] = n + e < p.N ? p.bias[n + e] : 0.f;
+      for (int e = 0; e < 4; ++e) bias[e] = n + e < p.N ? p.bias[batch * p.sBias + n + e] : 0.f;
 #pragma unroll
     for (int y = 0; y < 4; ++y) {
       const int m = m0 + wm * 64 + y * 16 + col;

@@ -12,7 +12,8 @@ struct GemmArgs {
   int64_t ldb, sB;
   void *C;
   int64_t ldc, sC;
-  const float *bias;        // [N] or null
+  const float *bias;        // [N] or null (batch b reads bias + b * sBias)
+  int64_t sBias;
   const void *aux;          // epilogue operand in C's dtype, or null
   int64_t ldaux, sAux, aux_rows;
   int M, N, K;

@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, BF16, BOOL = 0, 1, 2
 EPI_STORE, EPI_MUL_SIGMOID_AUX, EPI_SIGMOID_MUL_AUX, EPI_ACCUMULATE, EPI_MUL_SIGMOID_AUX_ACCUMULATE = range(5)
@@ -46,6 +46,7 @@ SIGNATURES = {
     "xfh_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _p]),
     "xfh_adaptive_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _i64, _f, _p, _i, _p]),
     "xfh_linear": (_i, [_p, _i64, _p, _p, _i64, _i64, _i64, _i, _p, _i64, _i, _i, _p, _i64, _i64, _p]),
+    "xfh_linear_batched": (_i, [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i, _p, _i64, _i64, _i, _p]),
     "xfh_glu_packed_rows": (_i64, [_i64]),
     "xfh_glu_pack_weight": (_i, [_p, _i64, _i64, _i, _p, _p]),
     "xfh_gated_linear_unit": (_i, [_p, _p, _i64, _i64, _i64, _i, _p, _i, _p]),
@@ -269,6 +270,38 @@ def fused_linear_weight(module: torch.nn.Module, names, dtype: torch.dtype) -> t
     if cache is None:
         cache = caches[tag] = FusedWeightCache()
     return cache.get([getattr(module, n).weight for n in names], dtype)
+
+
+class DerivedWeightCache:
+    """A tensor built from several parameters by ``build(*sources)`` (a one-time weight
+    preparation), re-made when any source changes (same keys as :class:`HipWeightCache`;
+    never cached when a source is an inference tensor)."""
+
+    def __init__(self):
+        self._key = None
+        self._sources = None
+        self._value = None
+
+    def get(self, sources, build):
+        try:
+            key = tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride()), t.dtype, t.device)
+                        for t in sources)
+        except RuntimeError:
+            self._key = self._sources = self._value = None
+            return build(*sources)
+        if self._key != key:
+            self._value = build(*sources)
+            self._sources = tuple(sources)
+            self._key = key
+        return self._value
+
+
+def derived_weight(module: torch.nn.Module, tag: str, sources, build):
+    caches = module.__dict__.setdefault("_hip_weight_caches", {})
+    cache = caches.get(tag)
+    if cache is None:
+        cache = caches[tag] = DerivedWeightCache()
+    return cache.get(list(sources), build)
 
 
 def fp32_param(module: torch.nn.Module, name: str, param: Optional[torch.Tensor]):

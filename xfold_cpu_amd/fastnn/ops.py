@@ -101,6 +101,31 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], 
     return out
 
 
+def linear_batched(x: torch.Tensor, weights: torch.Tensor, bias: Optional[torch.Tensor],
+                   dtype: torch.dtype, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``out[b] = x @ weights[b]^T + bias[b]`` in one launch: x [m, k] shared by every b (or
+    [B, m, k]), weights [B, n, k] already in the compute dtype, bias [B, n] (fp32) or None;
+    returns [B, m, n]."""
+    nb, n, k = weights.shape
+    if x.shape[-1] != k or not weights.is_contiguous():
+        raise ValueError("linear_batched: weights must be a contiguous [B, n, k] matching x")
+    shared = x.dim() == 2
+    if not shared and (x.dim() != 3 or x.shape[0] != nb):
+        raise ValueError("linear_batched: x must be [m, k] or [B, m, k]")
+    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    m = x_c.shape[-2]
+    out = torch.empty((nb, m, n), dtype=out_dtype or dtype, device=x.device)
+    b = None
+    if bias is not None:
+        if tuple(bias.shape) != (nb, n):
+            raise ValueError("linear_batched: bias must be [B, n]")
+        b = bias.detach().to(torch.float32).contiguous()
+    nh.call("xfh_linear_batched", nh.ptr(x_c), k, 0 if shared else m * k, nh.ptr(weights), n * k,
+            nh.ptr(b), n, m, k, n, nb, nh.dtype_code(dtype), nh.ptr(out), n, m * n,
+            nh.dtype_code(out.dtype), nh.stream_of(x.device))
+    return out
+
+
 def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torch.dtype,
                       out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """silu(x @ Wg) * (x @ Wv) from the packed weight (``xfold/fastnn/gated_linear_unit.py:103-107``)."""

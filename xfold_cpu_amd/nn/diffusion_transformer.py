@@ -23,12 +23,16 @@ from ..fastnn import ops
 
 
 def _adaptive_layer_norm(aln: nn.Module, x: torch.Tensor, single_cond: Optional[torch.Tensor],
-                         dtype: torch.dtype, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+                         dtype: torch.dtype, out_dtype: Optional[torch.dtype] = None,
+                         cond: Optional[tuple] = None) -> torch.Tensor:
     """``AdaptiveLayerNorm.forward`` (``diffusion_transformer.py:51-64``); Linears in
-    ``dtype``, result in ``out_dtype`` (default ``dtype``)."""
+    ``dtype``, result in ``out_dtype`` (default ``dtype``). ``cond`` = (scale, shift) already
+    computed from single_cond (see :func:`_block_conditioning`)."""
     if (single_cond is None) != (not aln.use_single_cond):
         raise ValueError("single_cond must be given exactly when use_single_cond is set")
     out_dtype = out_dtype or dtype
+    if cond is not None:
+        return ops.adaptive_layer_norm(x, cond[0], cond[1], aln.layer_norm.eps, out_dtype=out_dtype)
     if not aln.use_single_cond:
         ln = aln.layer_norm
         return ops.layer_norm(x, ln.normalized_shape, ln.weight, ln.bias, ln.eps, out_dtype=out_dtype,
@@ -43,15 +47,18 @@ def _adaptive_layer_norm(aln: nn.Module, x: torch.Tensor, single_cond: Optional[
 
 
 def _ada_ln_zero(zero: nn.Module, hidden: torch.Tensor, single_cond: Optional[torch.Tensor],
-                 dtype: torch.dtype, accumulate_into: Optional[torch.Tensor]) -> torch.Tensor:
-    """``AdaLNZero.forward`` (``diffusion_transformer.py:85-95``), optionally added in place."""
+                 dtype: torch.dtype, accumulate_into: Optional[torch.Tensor],
+                 cond: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``AdaLNZero.forward`` (``diffusion_transformer.py:85-95``), optionally added in place;
+    ``cond`` = adaptive_zero_cond(single_cond) already computed, in the output dtype."""
     w = nh.linear_weight(zero, "transition2", dtype)
     out = accumulate_into
     out_dtype = out.dtype if out is not None else dtype
     acc = out is not None
     if zero.use_single_cond:
-        cond = ops.linear(single_cond, nh.linear_weight(zero, "adaptive_zero_cond", dtype),
-                          zero.adaptive_zero_cond.bias, dtype, out_dtype=out_dtype)
+        if cond is None:
+            cond = ops.linear(single_cond, nh.linear_weight(zero, "adaptive_zero_cond", dtype),
+                              zero.adaptive_zero_cond.bias, dtype, out_dtype=out_dtype)
         epi = nh.EPI_MUL_SIGMOID_AUX_ACCUMULATE if acc else nh.EPI_MUL_SIGMOID_AUX
         return ops.linear(hidden, w, None, dtype, out=out, out_dtype=out_dtype, epilogue=epi,
                           aux=cond, aux_rows=cond.numel() // cond.shape[-1])
@@ -65,15 +72,19 @@ def _check_accumulate(out, x):
 
 
 def diffusion_transition_hip(module: nn.Module, x: torch.Tensor, single_cond=None,
-                             accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """``DiffusionTransition.forward`` (``diffusion_transformer.py:124-128``)."""
+                             accumulate_into: Optional[torch.Tensor] = None, *,
+                             _cond: Optional[tuple] = None) -> torch.Tensor:
+    """``DiffusionTransition.forward`` (``diffusion_transformer.py:124-128``). ``_cond`` =
+    (scale, shift, zero_cond) precomputed by :func:`_block_conditioning`."""
     nh.check_gpu_inference(x, single_cond, *module.parameters())
     dtype = nh.compute_dtype(x, module.transition1.weight)
     _check_accumulate(accumulate_into, x)
-    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype)
+    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype,
+                              cond=None if _cond is None else _cond[:2])
     f = module.transition1.weight.shape[0] // 2
     hidden = ops.gated_linear_unit(xn, nh.linear_weight(module, "transition1", dtype, "glu"), f, dtype)
-    return _ada_ln_zero(module.adaptive_zero_init, hidden, single_cond, dtype, accumulate_into)
+    return _ada_ln_zero(module.adaptive_zero_init, hidden, single_cond, dtype, accumulate_into,
+                        cond=None if _cond is None else _cond[2])
 
 
 _QKV = ("q_projection", "k_projection", "v_projection")
@@ -82,9 +93,11 @@ _QKV = ("q_projection", "k_projection", "v_projection")
 def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.Tensor],
                        pair_logits: Optional[torch.Tensor] = None,
                        single_cond: Optional[torch.Tensor] = None,
-                       accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
+                       accumulate_into: Optional[torch.Tensor] = None, *,
+                       _cond: Optional[tuple] = None) -> torch.Tensor:
     """``SelfAttention.forward`` (``diffusion_transformer.py:184-217``) for x [N, c] or
-    [S, N, c]; pair_logits [H, N, N] is the attention bias, mask [N] the key mask."""
+    [S, N, c]; pair_logits [H, N, N] is the attention bias, mask [N] the key mask.
+    ``_cond`` = (scale, shift, zero_cond) precomputed by :func:`_block_conditioning`."""
     nh.check_gpu_inference(x, mask, pair_logits, single_cond, *module.parameters())
     dtype = nh.compute_dtype(x, *(getattr(module, n).weight for n in _QKV + ("gating_query",)))
     _check_accumulate(accumulate_into, x)
@@ -94,7 +107,8 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     n, c = x.shape[-2], x.shape[-1]
     heads = module.num_head
     d = c // heads
-    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype)
+    xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype,
+                              cond=None if _cond is None else _cond[:2])
     w_qkv = nh.fused_linear_weight(module, _QKV, dtype)
     q_bias = module.q_projection.bias
     bias_qkv = None
@@ -122,7 +136,76 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     ops.linear(xn.reshape(samples, n, c), nh.linear_weight(module, "gating_query", dtype), None, dtype,
                out=o, epilogue=nh.EPI_SIGMOID_MUL_AUX, aux=o)
     o = o.reshape(x.shape)
-    return _ada_ln_zero(module.adaptive_zero_init, o, single_cond, dtype, accumulate_into)
+    return _ada_ln_zero(module.adaptive_zero_init, o, single_cond, dtype, accumulate_into,
+                        cond=None if _cond is None else _cond[2])
+
+
+def _conditioning_weights(module: nn.Module, alns, zeros, dtype: torch.dtype):
+    """Stacked conditioning weights of every block (a cached one-time weight preparation):
+    ([2A, c, c_s] scale/shift weights with the single_cond LayerNorm's weight folded into
+    their input columns, [2A, c] fp32 biases, [Z, c, c_s] adaptive_zero_cond weights, [Z, c]
+    biases). LayerNorm(s) = s_hat * g + b, so Linear(LayerNorm(s)) = s_hat (W g)^T + (W b + bias)."""
+    srcs = []
+    for a in alns:
+        cln = a.single_cond_layer_norm
+        srcs += [t for t in (cln.weight, cln.bias, a.single_cond_scale.weight, a.single_cond_scale.bias,
+                             a.single_cond_bias.weight, a.single_cond_bias.bias) if t is not None]
+    for z in zeros:
+        srcs += [t for t in (z.adaptive_zero_cond.weight, z.adaptive_zero_cond.bias) if t is not None]
+
+    def build(*_):
+        with torch.no_grad():
+            ws, bs = [], []
+            for a in alns:
+                cln = a.single_cond_layer_norm
+                for lin in (a.single_cond_scale, a.single_cond_bias):
+                    w = lin.weight.detach().float()
+                    b = (lin.bias.detach().float() if lin.bias is not None
+                         else torch.zeros(w.shape[0], dtype=torch.float32, device=w.device))
+                    if cln.bias is not None:
+                        b = b + w @ cln.bias.detach().float()
+                    ws.append(w * cln.weight.detach().float() if cln.weight is not None else w)
+                    bs.append(b)
+            zw = [z.adaptive_zero_cond.weight.detach().float() for z in zeros]
+            zb = [z.adaptive_zero_cond.bias.detach().float() if z.adaptive_zero_cond.bias is not None
+                  else torch.zeros(w.shape[0], dtype=torch.float32, device=w.device)
+                  for z, w in zip(zeros, zw)]
+            return (torch.stack(ws).to(dtype).contiguous(), torch.stack(bs).contiguous(),
+                    torch.stack(zw).to(dtype).contiguous(), torch.stack(zb).contiguous())
+
+    return nh.derived_weight(module, f"conditioning:{dtype}", srcs, build)
+
+
+def _block_conditioning(module: nn.Module, single_cond: torch.Tensor, dtype: torch.dtype,
+                        zero_dtype: torch.dtype):
+    """Every block's conditioning linears (``AdaptiveLayerNorm`` scale/shift,
+    ``diffusion_transformer.py:59-62``; ``AdaLNZero`` cond, ``:93``) computed up front: they
+    read only single_cond, which is the same for all blocks of one call. Two batched launches
+    (one over the normalised single_cond, one over single_cond itself) replace the 6 small
+    GEMMs of every block. Returns [(attention (scale, shift, zero), transition (...))] per
+    block, or None when some block has no single_cond conditioning (the per-block path)."""
+    n_blocks = len(module.self_attention)
+    att = [module.self_attention[i] for i in range(n_blocks)]
+    tr = [module.transition_block[i] for i in range(n_blocks)]
+    alns = [b.adaptive_layernorm for b in att] + [b.adaptive_layernorm for b in tr]
+    zeros = [b.adaptive_zero_init for b in att] + [b.adaptive_zero_init for b in tr]
+    if single_cond is None or not all(a.use_single_cond for a in alns) or \
+            not all(z.use_single_cond for z in zeros):
+        return None
+    eps = {a.single_cond_layer_norm.eps for a in alns}
+    shapes = {tuple(a.single_cond_layer_norm.normalized_shape) for a in alns}
+    if len(eps) != 1 or len(shapes) != 1:
+        return None
+    w_ss, b_ss, w_z, b_z = _conditioning_weights(module, alns, zeros, dtype)
+    s_hat = ops.layer_norm(single_cond, shapes.pop(), None, None, eps.pop(), out_dtype=dtype)
+    ss = ops.linear_batched(s_hat.reshape(-1, s_hat.shape[-1]), w_ss, b_ss, dtype)
+    zz = ops.linear_batched(single_cond.reshape(-1, single_cond.shape[-1]), w_z, b_z, dtype,
+                            out_dtype=zero_dtype)
+    lead = single_cond.shape[:-1]
+    view = lambda t: t.reshape(*lead, t.shape[-1])
+    return [((view(ss[2 * i]), view(ss[2 * i + 1]), view(zz[i])),
+             (view(ss[2 * (n_blocks + i)]), view(ss[2 * (n_blocks + i) + 1]), view(zz[n_blocks + i])))
+            for i in range(n_blocks)]
 
 
 def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.Tensor,
@@ -137,6 +220,7 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
     pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
                               out_dtype=dtype, owner=ln)
     heads, size = module.num_head, module.super_block_size
+    conds = _block_conditioning(module, single_cond, dtype, act.dtype)
     for s in range(module.num_super_blocks):
         weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
         logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]
@@ -144,10 +228,11 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         for j in range(size):
             bias = logits[..., j * heads:(j + 1) * heads].permute(2, 0, 1)
             index = s * size + j
+            att_cond, tr_cond = (None, None) if conds is None else conds[index]
             self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
-                               accumulate_into=act)
+                               accumulate_into=act, _cond=att_cond)
             diffusion_transition_hip(module.transition_block[index], act, single_cond,
-                                     accumulate_into=act)
+                                     accumulate_into=act, _cond=tr_cond)
     return act
 
 
