@@ -200,7 +200,7 @@ int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu
   if (p.M == 0 || p.N == 0 || batch == 0) return XFH_OK;
   if (p.M < 0 || p.N < 0 || p.K < 0) return fail(XFH_EINVAL, "gemm: negative size");
   if (int64_t(ceil_div(p.M, BM)) > 65535) return fail(XFH_EUNSUPPORTED, "gemm: M too large for one launch");
-  if (dtype == XFH_BF16 && (out_dtype == XFH_BF16 || out_dtype == XFH_F32) && ceil_div(p.N, 128) <= 65535 &&
+  if (dtype == XFH_BF16 && (out_dtype == XFH_BF16 || out_dtype == XFH_F32) && ceil_div(p.N, 64) <= 65535 &&
       batch <= 65535 && gemm_ring_supported(p, out_dtype))
     return gemm_ring(p, batch, out_dtype, glu, s);
   if (dtype == XFH_BF16 && out_dtype == XFH_BF16) return launch_typed<bf16, bf16>(p, batch, glu, s);

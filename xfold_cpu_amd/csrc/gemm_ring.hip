@@ -2,16 +2,19 @@
 // the projections and transitions (k a multiple of 32, 16-byte aligned rows). Same contract
 // as gemm_nt (gemm.hip), which keeps every other case.
 //
-// Tiling: 128 x 128 output tile per workgroup, 4 wavefronts in a 2 x 2 grid each owning
-// 64 x 64 (4 x 4 MFMA 16x16x32 tiles). Per k-step of 32 both 128 x 32 operand tiles go
-// global -> LDS with direct loads (global_load_lds_dwordx4, no registers) into a 4-slot
-// ring: the loads of steps s+1..s+3 are in flight while step s is multiplied, one barrier
-// per step. Rows are 64 B in LDS with the 16-byte slots XOR-swizzled (slot c of row r
-// holds chunk c ^ ((r >> 2) & 3)) so the 16 rows of an MFMA operand read hit distinct
-// bank groups. Rows past M or N read the last row (their results are never stored).
+// Tiling: 128 x BN output tile per workgroup (BN = 64, 96 or 128), 4 wavefronts in a 2 x 2
+// grid each owning 64 x BN/2 (4 x BN/32 MFMA 16x16x32 tiles). Per k-step of TK (32 or 64)
+// both operand tiles go global -> LDS with direct loads (global_load_lds_dwordx4, no
+// registers) into a ring of SLOTS stages: the loads of steps s+1 .. s+SLOTS-1 are in
+// flight while step s is multiplied, one barrier per step. A TK-deep row is CH = TK/8
+// 16-byte chunks; chunk c of row r sits in slot c ^ sw(r), sw(r) = (r / (16 / CH)) % CH,
+// so the 16 rows of an MFMA operand read (one chunk each) hit 16 distinct bank groups.
+// Rows past M or N read the last row (their results are never stored).
 // The MFMA takes the B rows as its A operand, so a lane ends up with four consecutive
 // output columns of one row: bias, auxiliary operand, accumulation and the GLU pairing
 // all work on 4-element vectors and the stores are 8 (bf16) or 16 (fp32) bytes.
+// The launcher picks the tile width, depth and ring from the problem's shape (more
+// workgroups for narrow outputs, deeper k-steps when k allows).
 #include "common.h"
 #include "kernels.h"
 
@@ -19,15 +22,22 @@ namespace xfh {
 
 namespace {
 
-constexpr int TB = 128;                  // tile edge
-constexpr int TK = 32;                   // k-step
-constexpr int SLOTS = 4;                 // ring of operand stages
-constexpr int OP_ELEMS = TB * TK;        // one operand tile (bf16), 8 KB
-constexpr int SLOT_ELEMS = 2 * OP_ELEMS;
-constexpr int PIECES = 2 * TB / 16;      // 1 KB loads per k-step (16), 4 per wavefront
-constexpr int PIECES_PER_WAVE = PIECES / 4;
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
+
+template <int BN_, int TK_, int SLOTS_, int WGS_> struct Ring {
+  static constexpr int BM = 128, BN = BN_, TK = TK_, SLOTS = SLOTS_, WGS = WGS_;
+  static constexpr int CH = TK / 8;                   // 16-byte chunks per LDS row
+  static constexpr int ROWS_PER_PIECE = 1024 / (2 * TK);   // rows per 1 KB direct load
+  static constexpr int PIECES = (BM + BN) / ROWS_PER_PIECE; // per k-step
+  static constexpr int PPW = PIECES / 4;              // per wavefront
+  static constexpr int NT = BN / 32;                  // MFMA tiles per wavefront along n
+  static constexpr int KS = TK / 32;                  // MFMA k-substeps per k-step
+  static constexpr int SLOT_ELEMS = (BM + BN) * TK;
+  static_assert(PIECES % 4 == 0, "direct-load pieces must split evenly over 4 wavefronts");
+  static_assert(SLOTS * SLOT_ELEMS * 2 * WGS <= 160 * 1024, "LDS budget");
+  __host__ __device__ static constexpr int sw(int r) { return (r / (16 / CH)) % CH; }
+};
 
 template <int N> __device__ __forceinline__ void wait_vmcnt() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -67,48 +77,62 @@ __device__ __forceinline__ float epilogue(int epi, float acc, float c, float aux
   }
 }
 
-template <typename TO, bool GLU>
-__global__ __launch_bounds__(256, 2) void gemm_ring_kernel(GemmArgs p) {
-  __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * SLOT_ELEMS];
+template <class G, int N> __device__ __forceinline__ void wait_younger(int younger) {
+  // Waits until at most `younger` k-steps of this wavefront's loads are in flight.
+  if constexpr (N == 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (younger >= N) wait_vmcnt<N * G::PPW>();
+    else wait_younger<G, N - 1>(younger);
+  }
+}
+
+template <typename TO, bool GLU, class G>
+__global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
+  constexpr int BM = G::BM, BN = G::BN, TK = G::TK, SLOTS = G::SLOTS, CH = G::CH, NT = G::NT;
+  constexpr int RPP = G::ROWS_PER_PIECE, PPW = G::PPW, WN = BN / 2;
+  __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * G::SLOT_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
-  const int m0 = blockIdx.y * TB, n0 = blockIdx.x * TB;
+  const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
   const int64_t batch = blockIdx.z;
   const bf16 *A = static_cast<const bf16 *>(p.A) + batch * p.sA;
   const bf16 *B = static_cast<const bf16 *>(p.B) + batch * p.sB;
 
-  // Piece q of a k-step: operand q / 8 (A, B), rows 16 (q % 8) .. +15; lane -> row
-  // 16 (q % 8) + lane / 4, LDS slot lane % 4 holding chunk (lane % 4) ^ ((lane >> 4) & 3).
-  const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
-  const bf16 *src[PIECES_PER_WAVE];
+  // Piece q of a k-step covers rows RPP q .. of the [A rows; B rows] stage; lane -> row
+  // RPP q + lane / CH, LDS slot lane % CH holding chunk (lane % CH) ^ sw(row).
+  const bf16 *src[PPW];
 #pragma unroll
-  for (int j = 0; j < PIECES_PER_WAVE; ++j) {
+  for (int j = 0; j < PPW; ++j) {
     const int q = wave + 4 * j;
-    const int row = (q % 8) * 16 + (lane >> 2);
-    if (q < 8) {
+    const int row = q * RPP + lane / CH;
+    const int chunk = (lane % CH) ^ G::sw(row);
+    if (row < BM) {
       const int m = m0 + row;
       src[j] = A + int64_t(m < p.M ? m : p.M - 1) * p.lda + chunk * 8;
     } else {
-      const int n = n0 + row;
+      const int n = n0 + row - BM;
       src[j] = B + int64_t(n < p.N ? n : p.N - 1) * p.ldb + chunk * 8;
     }
   }
   auto issue = [&](int step, int slot) {
 #pragma unroll
-    for (int j = 0; j < PIECES_PER_WAVE; ++j) {
+    for (int j = 0; j < PPW; ++j) {
       const int q = wave + 4 * j;
-      bf16 *dst = lds + slot * SLOT_ELEMS + (q < 8 ? 0 : OP_ELEMS) + (q % 8) * 16 * TK;
+      bf16 *dst = lds + slot * G::SLOT_ELEMS + q * RPP * TK;
       __builtin_amdgcn_global_load_lds((global_void *)(src[j] + step * TK), (lds_void *)dst, 16, 0, 0);
     }
   };
 
-  // Fragment offset: row base + col of an operand tile, k-chunk grp, lives at
-  // row * TK + (grp ^ ((col >> 2) & 3)) * 8 for a base that is a multiple of 16.
-  const int frag = col * TK + ((grp ^ ((col >> 2) & 3)) * 8);
-
-  f32x4 acc[4][4];   // [jt][it]: rows n (A operand = B rows), cols m (B operand = A rows)
+  // Fragment offset of (row base + col, k-substep ks, chunk 4 ks + grp) for a row base that
+  // is a multiple of 16: the swizzle depends on col only.
+  int frag[G::KS];
 #pragma unroll
-  for (int x = 0; x < 4; ++x)
+  for (int ks = 0; ks < G::KS; ++ks) frag[ks] = col * TK + ((4 * ks + grp) ^ G::sw(col)) * 8;
+
+  f32x4 acc[NT][4];   // [x][y]: rows n (A operand = B rows), cols m (B operand = A rows)
+#pragma unroll
+  for (int x = 0; x < NT; ++x)
 #pragma unroll
     for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
@@ -120,31 +144,33 @@ __global__ __launch_bounds__(256, 2) void gemm_ring_kernel(GemmArgs p) {
     // This wavefront's loads of step s have landed (the younger steps may still fly), then
     // every wavefront's have, and every wavefront is done with step s - 1.
     const int younger = steps - 1 - s;
-    if (younger >= 2) wait_vmcnt<2 * PIECES_PER_WAVE>();
-    else if (younger == 1) wait_vmcnt<PIECES_PER_WAVE>();
-    else wait_vmcnt<0>();
+    wait_younger<G, SLOTS - 2>(younger);
     __syncthreads();
     if (s + SLOTS - 1 < steps) issue(s + SLOTS - 1, (s + SLOTS - 1) % SLOTS);
-    const bf16 *ta = lds + (s % SLOTS) * SLOT_ELEMS, *tb = ta + OP_ELEMS;
-    bf16x8 fa[4], fb[4];
+    const bf16 *ta = lds + (s % SLOTS) * G::SLOT_ELEMS, *tb = ta + BM * TK;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * 64 + y * 16) * TK + frag);
+    for (int ks = 0; ks < G::KS; ++ks) {
+      bf16x8 fa[4], fb[NT];
 #pragma unroll
-    for (int x = 0; x < 4; ++x) {
-      fb[x] = *reinterpret_cast<const bf16x8 *>(tb + (wn * 64 + x * 16) * TK + frag);
+      for (int y = 0; y < 4; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * 64 + y * 16) * TK + frag[ks]);
 #pragma unroll
-      for (int y = 0; y < 4; ++y) acc[x][y] = mfma16(fb[x], fa[y], acc[x][y]);
+      for (int x = 0; x < NT; ++x) {
+        fb[x] = *reinterpret_cast<const bf16x8 *>(tb + (wn * WN + x * 16) * TK + frag[ks]);
+#pragma unroll
+        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16(fb[x], fa[y], acc[x][y]);
+      }
     }
   }
 
-  // acc[x][y][e] = C[m = m0 + wm*64 + y*16 + col][n = n0 + wn*64 + x*16 + grp*4 + e]
+  // acc[x][y][e] = C[m = m0 + wm*64 + y*16 + col][n = n0 + wn*WN + x*16 + grp*4 + e]
   TO *C = static_cast<TO *>(p.C) + batch * p.sC;
   if constexpr (GLU) {
     // Packed GLU weight: 32-column groups = 16 gate columns then the 16 matching value
     // columns, so tiles (0, 1) and (2, 3) of a wavefront hold gate/value of the same features.
+    static_assert(!GLU || NT % 2 == 0, "GLU pairs whole 32-column groups");
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int f = (n0 + wn * 64) / 2 + q * 16 + grp * 4;
+    for (int q = 0; q < NT / 2; ++q) {
+      const int f = (n0 + wn * WN) / 2 + q * 16 + grp * 4;
 #pragma unroll
       for (int y = 0; y < 4; ++y) {
         const int m = m0 + wm * 64 + y * 16 + col;
@@ -166,8 +192,8 @@ __global__ __launch_bounds__(256, 2) void gemm_ring_kernel(GemmArgs p) {
   }
   const TO *aux = static_cast<const TO *>(p.aux);
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    const int n = n0 + wn * 64 + x * 16 + grp * 4;
+  for (int x = 0; x < NT; ++x) {
+    const int n = n0 + wn * WN + x * 16 + grp * 4;
     if (n >= p.N) continue;
     const bool full = n + 4 <= p.N;
     float bias[4] = {0.f, 0.f, 0.f, 0.f};
@@ -214,25 +240,71 @@ bool aligned(const void *ptr, int bytes) { return reinterpret_cast<uintptr_t>(pt
 
 }  // namespace
 
+// Ring configurations (tile width, k-step, stages, workgroups per CU).
+using RingWide = Ring<128, 64, 2, 2>;     // wide outputs, k % 64 == 0
+using RingMid = Ring<96, 64, 2, 2>;       // 3/4-width tiles: more workgroups for narrow outputs
+using RingNarrow = Ring<64, 64, 3, 2>;    // N <= 64, or too few workgroups otherwise
+using RingShallow = Ring<128, 32, 4, 2>;  // k % 64 != 0
+using RingShallowNarrow = Ring<64, 32, 4, 2>;
+
+template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
+  const dim3 grid(unsigned(ceil_div(p.N, G::BN)), unsigned(ceil_div(p.M, G::BM)), unsigned(batch));
+  if (glu) {
+    if constexpr (G::NT % 2 == 0) {
+      if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G><<<grid, 256, 0, s>>>(p);
+      else gemm_ring_kernel<float, true, G><<<grid, 256, 0, s>>>(p);
+    } else {
+      return fail(XFH_EUNSUPPORTED, "gemm_ring: GLU needs whole 32-column groups per wavefront");
+    }
+  } else {
+    if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, false, G><<<grid, 256, 0, s>>>(p);
+    else gemm_ring_kernel<float, false, G><<<grid, 256, 0, s>>>(p);
+  }
+  return check_launch("gemm_ring");
+}
+
+enum class RingPick { Wide, Mid, Narrow, Shallow, ShallowNarrow };
+
+// Tile width: the 64-column tile (the only one with a 3-stage ring at two workgroups per
+// CU) unless the grid then needs more rounds of workgroups than a wider tile would, rounds
+// weighted by the tile's width (measured on the diffusion transformer's Linears: the
+// 64-column tile is fastest whenever it fits in one round, the 96-column tile on
+// 3840 x 2304 outputs). 64-deep k-steps when k allows. GLU pairs whole 32-column groups per
+// wavefront, so it takes 64 or 128.
+RingPick pick_ring(const GemmArgs &p, int64_t batch, bool glu, int cus) {
+  const int64_t mt = ceil_div(p.M, 128) * batch, slots = 2 * int64_t(cus);
+  auto rounds = [&](int bn) { return ceil_div(mt * ceil_div(p.N, bn), slots); };
+  if (p.K % 64 != 0) return (p.N <= 64 || rounds(64) <= 1) ? RingPick::ShallowNarrow : RingPick::Shallow;
+  if (p.N <= 64 || rounds(64) <= 1) return RingPick::Narrow;
+  RingPick best = RingPick::Narrow;
+  int64_t cost = rounds(64) * 64;
+  if (!glu && rounds(96) * 96 <= cost) {
+    best = RingPick::Mid;
+    cost = rounds(96) * 96;
+  }
+  if (rounds(128) * 128 < cost) best = RingPick::Wide;
+  return best;
+}
+
 bool gemm_ring_supported(const GemmArgs &p, int out_dtype) {
   const int ob = out_dtype == XFH_BF16 ? 2 : 4;
   const bool vec_out = p.ldc % 4 == 0 && p.sC % 4 == 0 && aligned(p.C, 4 * ob) &&
                        (!p.aux || (p.ldaux % 4 == 0 && p.sAux % 4 == 0 && aligned(p.aux, 4 * ob)));
-  return p.K > 0 && p.K % TK == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sA % 8 == 0 &&
+  return p.K > 0 && p.K % 32 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sA % 8 == 0 &&
          p.sB % 8 == 0 && aligned(p.A, 16) && aligned(p.B, 16) && vec_out;
 }
 
 int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
-  const dim3 grid(unsigned(ceil_div(p.N, TB)), unsigned(ceil_div(p.M, TB)), unsigned(batch));
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
   KernelTimer timer("gemm_ring", s);
-  if (out_dtype == XFH_BF16) {
-    if (glu) gemm_ring_kernel<bf16, true><<<grid, 256, 0, s>>>(p);
-    else gemm_ring_kernel<bf16, false><<<grid, 256, 0, s>>>(p);
-  } else {
-    if (glu) gemm_ring_kernel<float, true><<<grid, 256, 0, s>>>(p);
-    else gemm_ring_kernel<float, false><<<grid, 256, 0, s>>>(p);
+  switch (pick_ring(p, batch, glu, cus)) {
+    case RingPick::Wide: return launch_ring<RingWide>(p, batch, out_dtype, glu, s);
+    case RingPick::Mid: return launch_ring<RingMid>(p, batch, out_dtype, glu, s);
+    case RingPick::Narrow: return launch_ring<RingNarrow>(p, batch, out_dtype, glu, s);
+    case RingPick::Shallow: return launch_ring<RingShallow>(p, batch, out_dtype, glu, s);
+    default: return launch_ring<RingShallowNarrow>(p, batch, out_dtype, glu, s);
   }
-  return check_launch("gemm_ring");
 }
 
 }  // namespace xfh
