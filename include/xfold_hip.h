@@ -26,10 +26,13 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 3
+#define XFH_ABI_VERSION 4
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
+
+/* Bias "dtype" of xfh_dot_product_attention for a bias written by xfh_attention_bias_pack. */
+#define XFH_BIAS_PACKED 3
 
 /* GEMM epilogues of xfh_linear: acc = x @ w^T + bias, a = aux[row % aux_rows, col]. */
 enum {
@@ -118,12 +121,26 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
  * With bf16 inputs and output, head dims <= 64, a bias shared by the batch entries and a
  * mask that depends on the batch entry and key only (the single-track and diffusion
  * shapes), a workspace of xfh_dot_product_attention_workspace_size(shape, dtype) bytes
- * selects the pipelined kernel; other calls, or workspace = NULL, use the general one. */
+ * selects the pipelined kernel; other calls, or workspace = NULL, use the general one.
+ * bias_dtype = XFH_BIAS_PACKED: bias points at one [H][Q][align64(K)] block written by
+ * xfh_attention_bias_pack (bias strides ignored); such calls must take the pipelined kernel
+ * and fail with XFH_EUNSUPPORTED otherwise. */
 int64_t xfh_dot_product_attention_workspace_size(const int64_t *shape, int dtype);
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
                               void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
                               float scale, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Converts G attention biases, bias[g][h][q][k] (shape = {G, H, Q, K}, strides in
+ * elements, f32 or bf16), into the pipelined attention kernel's layout once:
+ * packed[g][h][q][k'] fp32 = bias * log2(e) for k' < K, 0 for K <= k' < align64(K)
+ * (packed holds G*H*Q*align64(K) floats). Block g is then passed to
+ * xfh_dot_product_attention with bias_dtype XFH_BIAS_PACKED. No counterpart in the
+ * reference: the DiffusionTransformer's pair logits (xfold/nn/diffusion_transformer.py:
+ * 258-271) feed the attention biases of a whole super-block, which it converts once
+ * instead of once per block. */
+int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides,
+                            void *packed, void *stream);
 
 /* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).
  * out (contiguous [n, n, c]) receives the update, or the update is added to it when

@@ -48,6 +48,15 @@ def test_invalid_arguments_fail_before_any_launch():
         nh.call("xfh_linear", None, 4, None, None, 4, 4, 4, 0, None, 4, 0, nh.EPI_MUL_SIGMOID_AUX, None, 4, 0, None)
     with pytest.raises(ValueError, match="overlap"):
         nh.call("xfh_linear_batched", None, 4, 0, None, 16, None, 0, 4, 4, 4, 2, 0, None, 4, 8, 0, None)
+    with pytest.raises(ValueError, match="dtype"):
+        nh.call("xfh_attention_bias_pack", None, 7, (ctypes.c_int64 * 4)(1, 1, 4, 4),
+                (ctypes.c_int64 * 4)(16, 16, 4, 1), None, None)
+    # A packed bias off the pipelined kernel (fp32 inputs) is refused before any launch.
+    fake = ctypes.c_void_p(1 << 40)
+    shape6 = (ctypes.c_int64 * 6)(1, 1, 8, 8, 8, 8)
+    with pytest.raises(ValueError, match="packed bias"):
+        nh.call("xfh_dot_product_attention", fake, fake, fake, nh.F32, None, 2, fake, nh.BIAS_PACKED, fake,
+                nh.F32, shape6, (ctypes.c_int64 * 20)(), 1.0, None, 0, None)
     with pytest.raises(ValueError, match="head dim"):
         nh.call("xfh_grid_self_attention", None, 0, None, 2, 8, 512, 4, 0, None, None, 1e-5,
                 None, None, None, None, None, None, 0, None, 0, 0, None, 0, None)

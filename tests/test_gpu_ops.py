@@ -176,6 +176,31 @@ def test_gated_linear_unit(device, m, k, f, dtype):
 
 # ---------------------------------------------------------------------------- attention
 
+@pytest.mark.parametrize("d", [32, 48, 64])
+@pytest.mark.parametrize("head_minor", [True, False])
+def test_attention_packed_bias(device, d, head_minor):
+    """A bias converted once by attention_bias_pack (head-minor bf16 logits, as the
+    diffusion transformer's super-block, or strided fp32) gives bit-identical attention to
+    passing the same bias per call."""
+    announce("attention packed bias", d, head_minor)
+    g = torch.Generator().manual_seed(d)
+    B, H, N, G = 3, 4, 100, 2
+    q, k, v = (torch.randn(B, H, N, d, generator=g).bfloat16().to(device) for _ in range(3))
+    mask = (torch.rand(B, N, generator=g) > 0.2).to(device)
+    mask[1] = False                                   # a fully masked batch entry
+    if head_minor:
+        logits = torch.randn(N, N, G * H, generator=g).bfloat16().to(device)
+        biases = logits.view(N, N, G, H).permute(2, 3, 0, 1)
+    else:
+        biases = torch.randn(G, H, N, N, generator=g).to(device)
+    packed = ops.attention_bias_pack(biases)
+    assert packed.shape == (G, H, N, 128) and bool((packed[..., N:] == 0).all())
+    for j in range(G):
+        want = ops.attention(q, k, v, mask, biases[j])
+        got = ops.attention(q, k, v, mask, ops.PackedBias(packed[j]))
+        assert torch.equal(got, want), f"block {j}: max diff {(got.float() - want.float()).abs().max().item()}"
+
+
 @pytest.mark.parametrize("mask_rank", [1, 2, 4])
 @pytest.mark.parametrize("batched", [True, False])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

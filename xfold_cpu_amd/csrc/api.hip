@@ -302,7 +302,8 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   XFH_REQUIRE(shape && strides, "dot_product_attention: null shape/strides");
   XFH_REQUIRE(float_dtype(dtype), "dot_product_attention: dtype must be f32/bf16");
   XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "dot_product_attention: bad mask dtype");
-  XFH_REQUIRE(!bias || float_dtype(bias_dtype), "dot_product_attention: bias must be f32/bf16");
+  XFH_REQUIRE(!bias || float_dtype(bias_dtype) || bias_dtype == XFH_BIAS_PACKED,
+              "dot_product_attention: bias must be f32/bf16 or packed");
   AttentionArgs a;
   std::memset(&a, 0, sizeof(a));
   a.q = q; a.k = k; a.v = v; a.o = out;
@@ -323,7 +324,21 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   // workspace of xfh_dot_product_attention_workspace_size bytes; the rest, or a call
   // without workspace, on the general kernel.
   if (workspace && mha_supported(a, dtype)) return mha(a, workspace, workspace_bytes, as_stream(stream));
+  if (bias && bias_dtype == XFH_BIAS_PACKED)
+    return fail(XFH_EUNSUPPORTED, "dot_product_attention: a packed bias needs the pipelined kernel "
+                                  "(bf16, head dim <= 64, workspace given)");
   return attention(a, dtype, as_stream(stream));
+}
+
+int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides,
+                            void *packed, void *stream) {
+  XFH_REQUIRE(shape && strides, "attention_bias_pack: null shape/strides");
+  XFH_REQUIRE(float_dtype(dtype), "attention_bias_pack: dtype must be f32/bf16");
+  for (int i = 0; i < 4; ++i) XFH_REQUIRE(shape[i] >= 0, "attention_bias_pack: negative size");
+  XFH_REQUIRE(shape[3] <= grid_attention_max_n(), "attention_bias_pack: more keys than the attention kernel takes");
+  if (shape[0] * shape[1] * shape[2] * shape[3] == 0) return XFH_OK;
+  XFH_REQUIRE(bias && packed, "attention_bias_pack: null tensor");
+  return attention_bias_pack(bias, dtype, shape, strides, packed, as_stream(stream));
 }
 
 int64_t xfh_triangle_multiplication_workspace_size(int64_t n, int64_t c, int dtype) {

@@ -52,6 +52,8 @@ int attention(const AttentionArgs &a, int dtype, hipStream_t s);
 int64_t mha_workspace_size(const AttentionArgs &a);
 bool mha_supported(const AttentionArgs &a, int dtype);
 int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStream_t s);
+int attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides, void *packed,
+                        hipStream_t s);
 
 // Triangle (grid) attention, bf16, head dim 32 (grid_attention.hip).
 // Layouts (D = padded head dim, 32 or 64): q [B][H][Nq][D] pre-scaled by d^-0.5 * log2(e);

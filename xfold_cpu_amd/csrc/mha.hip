@@ -167,7 +167,7 @@ int64_t mha_workspace_size(const AttentionArgs &a) {
 bool mha_supported(const AttentionArgs &a, int dtype) {
   return dtype == XFH_BF16 && a.out_dtype == XFH_BF16 && padded_dim(a.D > a.Dv ? a.D : a.Dv) != 0 &&
          a.K > 0 && align_up(a.K, 64) <= grid_attention_max_n() &&
-         (!a.bias || a.B == 1 || a.bs[0] == 0) &&           // bias shared by the batch entries
+         (!a.bias || a.bias_dtype == XFH_BIAS_PACKED || a.B == 1 || a.bs[0] == 0) &&  // batch-shared bias
          (!a.mask || (a.ms[1] == 0 && a.ms[2] == 0)) &&      // mask per (batch entry, key)
          a.os[1] % 4 == 0 && a.os[2] % 4 == 0 && a.os[0] % 4 == 0 &&
          reinterpret_cast<uintptr_t>(a.o) % 8 == 0;
@@ -199,7 +199,9 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
   const bool head_minor = a.bias && a.bias_dtype == XFH_BF16 && a.bs[1] == 1 && a.H % 8 == 0 &&
                           a.bs[2] % 8 == 0 && a.bs[3] % 8 == 0 &&
                           reinterpret_cast<uintptr_t>(a.bias) % 16 == 0;
+  const bool packed = a.bias && a.bias_dtype == XFH_BIAS_PACKED;
   for (int part = 0; part < 5; ++part) {
+    if (part == 3 && packed) continue;             // already in the kernel's layout
     const int64_t n_work = part == 3 && head_minor ? a.Q * pl.npad : work[part];
     const int64_t blocks = ceil_div(n_work, 256);
     if (blocks == 0) continue;
@@ -209,13 +211,77 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
   XFH_TRY(check_launch("mha_prepare"));
 
   GridAttentionArgs ga;
-  ga.q = p.q; ga.k = p.k; ga.vt = p.vt; ga.bias = p.bias; ga.maskbits = p.words;
+  ga.q = p.q; ga.k = p.k; ga.vt = p.vt; ga.maskbits = p.words;
+  ga.bias = packed ? static_cast<const float *>(a.bias) : p.bias;
   ga.out = static_cast<bf16 *>(a.o);
   ga.osb = a.os[0]; ga.ost = a.os[2]; ga.ohs = a.os[1];
   ga.mbs = per_row ? pl.nblk : 0;
   ga.B = int(a.B); ga.H = int(a.H); ga.Nq = int(a.Q); ga.N = int(a.K);
   ga.Npad = int(pl.npad); ga.Nblk = int(pl.nblk); ga.Dv = int(a.Dv);
   return mha_attention(ga, pl.D, s);
+}
+
+namespace {
+
+// Bias packing: thread = (q, key) over keys < npad, reading all G*H heads of a bf16 view whose
+// heads are innermost (g stride H, h stride 1) 8 at a time.
+__global__ void bias_pack_head_minor_kernel(const bf16 *__restrict__ src, int64_t sq, int64_t sk, int gh,
+                                            int64_t Q, int64_t K, int64_t npad, float *__restrict__ dst) {
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= Q * npad) return;
+  const int64_t key = idx % npad, q = idx / npad;
+  const bf16 *row = src + q * sq + key * sk;
+  float *out = dst + q * npad + key;
+  const int64_t plane = Q * npad;
+  for (int c = 0; c < gh; c += 8) {
+    bf16x8 v = {};
+    if (key < K) v = *reinterpret_cast<const bf16x8 *>(row + c);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) out[(c + e) * plane] = static_cast<float>(v[e]) * kLog2eF;
+  }
+}
+
+// Any strides: thread = (g*H + h, q, 4 keys).
+__global__ void bias_pack_kernel(const void *__restrict__ src, int dtype, int64_t H, int64_t sg, int64_t sh,
+                                 int64_t sq, int64_t sk, int64_t GH, int64_t Q, int64_t K, int64_t npad,
+                                 float *__restrict__ dst) {
+  const int64_t quads = npad / 4;
+  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= GH * Q * quads) return;
+  const int64_t kq = idx % quads, row = idx / quads, q = row % Q, gh = row / Q;
+  const int64_t base = (gh / H) * sg + (gh % H) * sh + q * sq;
+  float v[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int64_t key = kq * 4 + e;
+    const int64_t off = base + key * sk;
+    v[e] = key < K ? (dtype == XFH_F32 ? ld<float>(src, off) : ld<bf16>(src, off)) * kLog2eF : 0.f;
+  }
+  *reinterpret_cast<float4 *>(dst + row * npad + kq * 4) = make_float4(v[0], v[1], v[2], v[3]);
+}
+
+}  // namespace
+
+int attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides, void *packed,
+                        hipStream_t s) {
+  const int64_t G = shape[0], H = shape[1], Q = shape[2], K = shape[3];
+  const int64_t npad = align_up(K, 64), GH = G * H;
+  if (GH * Q * npad == 0) return XFH_OK;
+  const bool head_minor = dtype == XFH_BF16 && strides[1] == 1 && strides[0] == H && GH % 8 == 0 &&
+                          strides[2] % 8 == 0 && strides[3] % 8 == 0 &&
+                          reinterpret_cast<uintptr_t>(bias) % 16 == 0;
+  if (head_minor) {
+    const int64_t blocks = ceil_div(Q * npad, 256);
+    if (blocks > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "attention_bias_pack: problem too large");
+    bias_pack_head_minor_kernel<<<dim3(unsigned(blocks)), 256, 0, s>>>(
+        static_cast<const bf16 *>(bias), strides[2], strides[3], int(GH), Q, K, npad, static_cast<float *>(packed));
+  } else {
+    const int64_t blocks = ceil_div(GH * Q * (npad / 4), 256);
+    if (blocks > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "attention_bias_pack: problem too large");
+    bias_pack_kernel<<<dim3(unsigned(blocks)), 256, 0, s>>>(bias, dtype, H, strides[0], strides[1], strides[2],
+                                                             strides[3], GH, Q, K, npad, static_cast<float *>(packed));
+  }
+  return check_launch("attention_bias_pack");
 }
 
 }  // namespace xfh

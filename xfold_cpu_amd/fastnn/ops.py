@@ -138,11 +138,37 @@ def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torc
     return y
 
 
+class PackedBias:
+    """One [H, Q, align64(K)] block of :func:`attention_bias_pack`'s output, passed to
+    :func:`attention` as its bias (the pipelined kernel reads it as it stands)."""
+
+    def __init__(self, tensor: torch.Tensor):
+        if tensor.dim() != 3 or tensor.dtype != torch.float32 or not tensor.is_contiguous():
+            raise ValueError("PackedBias wraps one contiguous fp32 [H, Q, align64(K)] block")
+        self.tensor = tensor
+
+
+def attention_bias_pack(bias: torch.Tensor) -> torch.Tensor:
+    """[G, H, Q, K] biases (fp32/bf16, any strides) -> [G, H, Q, align64(K)] fp32 in the
+    pipelined attention kernel's layout (times log2(e), zero pad), converted once for G calls."""
+    G, H, Q, K = bias.shape
+    if bias.dtype not in (torch.float32, torch.bfloat16):
+        bias = bias.to(torch.float32)
+    npad = (K + 63) // 64 * 64
+    out = torch.empty((G, H, Q, npad), dtype=torch.float32, device=bias.device)
+    shape = (ctypes.c_int64 * 4)(G, H, Q, K)
+    strides = (ctypes.c_int64 * 4)(*bias.stride())
+    nh.call("xfh_attention_bias_pack", nh.ptr(bias), nh.dtype_code(bias.dtype), shape, strides, nh.ptr(out),
+            nh.stream_of(bias.device))
+    return out
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
               bias: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """4-D [B, H, N, D] strided q/k/v (last dim contiguous); mask/bias broadcast to
-    [B, H, Q, K] per ``xfold/fastnn/attention.py:45-66``."""
+    [B, H, Q, K] per ``xfold/fastnn/attention.py:45-66`` (bias may also be a
+    :class:`PackedBias`, shared by the batch)."""
     B, H, Q, D = q.shape
     K, Dv = k.shape[2], v.shape[3]
     if k.shape[:2] != (B, H) or v.shape[:3] != (B, H, K) or k.shape[3] != D:
@@ -173,7 +199,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
         mask_code = nh.BOOL
         mask_strides = tuple(mask_t.stride())
     bias_t, bias_code, bias_strides = None, nh.F32, (0, 0, 0, 0)
-    if bias is not None:
+    if isinstance(bias, PackedBias):
+        if tuple(bias.tensor.shape) != (H, Q, (K + 63) // 64 * 64):
+            raise ValueError("attention: packed bias does not match [H, Q, align64(K)]")
+        bias_t, bias_code = bias.tensor, nh.BIAS_PACKED
+    elif bias is not None:
         if bias.dtype not in (torch.float32, torch.bfloat16):
             bias = bias.to(torch.float32)
         bias_t = bias.expand(B, H, Q, K)

@@ -98,7 +98,8 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     """``SelfAttention.forward`` (``diffusion_transformer.py:184-217``) for x [N, c] or
     [S, N, c]; pair_logits [H, N, N] is the attention bias, mask [N] the key mask.
     ``_cond`` = (scale, shift, zero_cond) precomputed by :func:`_block_conditioning`."""
-    nh.check_gpu_inference(x, mask, pair_logits, single_cond, *module.parameters())
+    logits_t = pair_logits.tensor if isinstance(pair_logits, ops.PackedBias) else pair_logits
+    nh.check_gpu_inference(x, mask, logits_t, single_cond, *module.parameters())
     dtype = nh.compute_dtype(x, *(getattr(module, n).weight for n in _QKV + ("gating_query",)))
     _check_accumulate(accumulate_into, x)
     if x.dim() not in (2, 3):
@@ -130,7 +131,9 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     o = torch.empty((samples, n, c), dtype=dtype, device=x.device)
     o_view = torch.as_strided(o, (samples, heads, n, d), (n * c, d, c, 1), 0)
     bias = None
-    if pair_logits is not None:
+    if isinstance(pair_logits, ops.PackedBias):
+        bias = pair_logits
+    elif pair_logits is not None:
         bias = pair_logits if pair_logits.dim() == 4 else pair_logits.unsqueeze(0)
     ops.attention(views[0], views[1], views[2], mask, bias, out=o_view)
     ops.linear(xn.reshape(samples, n, c), nh.linear_weight(module, "gating_query", dtype), None, dtype,
@@ -221,12 +224,23 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
                               out_dtype=dtype, owner=ln)
     heads, size = module.num_head, module.super_block_size
     conds = _block_conditioning(module, single_cond, dtype, act.dtype)
+    if mask is not None and mask.dtype not in (torch.bool, torch.uint8):
+        mask = mask.to(torch.bool)      # once, not per block (xfold/fastnn/attention.py:57-61)
+    packed_bias = dtype == torch.bfloat16 and module.self_attention[0].num_head == heads and \
+        act.shape[-1] // heads <= 64
     for s in range(module.num_super_blocks):
         weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
         logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]
-        # 'n s (b h) -> b h n s': block j, head h reads column j*heads + h.
+        # 'n s (b h) -> b h n s': block j, head h reads column j*heads + h. On the pipelined
+        # attention path (bf16, head dim <= 64) the super-block's biases are converted once.
+        n_tok = logits.shape[0]
+        if packed_bias:
+            packed = ops.attention_bias_pack(logits.view(n_tok, n_tok, size, heads).permute(2, 3, 0, 1))
         for j in range(size):
-            bias = logits[..., j * heads:(j + 1) * heads].permute(2, 0, 1)
+            if packed_bias:
+                bias = ops.PackedBias(packed[j])
+            else:
+                bias = logits[..., j * heads:(j + 1) * heads].permute(2, 0, 1)
             index = s * size + j
             att_cond, tr_cond = (None, None) if conds is None else conds[index]
             self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
