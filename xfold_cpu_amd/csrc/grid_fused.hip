@@ -1,11 +1,11 @@
 // Fused projection and output kernels around the triangle-attention core (bf16 compute,
 // c = 128, 4 heads x 32), following GridSelfAttention.forward (xfold/nn/attention.py:80-105):
 //
-//   grid_project: LN(z) -> one GEMM over a packed [q | k | v | bias] weight -> q scaled by
-//       d^-0.5 * log2(e), k (rows up to npad, zero beyond n), v^T (zero beyond n, keys
-//       permuted in runs of 32) and the fp32 pair bias (times log2(e)),
-//       each written straight into the attention kernel's layout (grid_attention.hip).
-//       The bias comes from the un-transposed pair in both directions.
+//   grid_project: LN(z) -> GEMMs over the packed [q | k | v | bias] weight (resident in
+//       LDS) -> q scaled by d^-0.5 * log2(e), k (rows up to npad, zero beyond n), v^T (zero
+//       beyond n, keys permuted in runs of 32) and the fp32 pair bias (times log2(e)), each
+//       written straight into the attention kernel's layout (grid_attention.hip). The bias
+//       comes from the un-transposed pair in both directions.
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
 //       the residual) -> (gate * o) Wout^T -> z += update (or update stored).
 //   grid_prepare: the packed weight and the attention kernel's kept-key words, one launch.
@@ -25,128 +25,169 @@ using namespace panel;
 constexpr int HD = 32;                 // head dim
 constexpr int QKV_ROWS = 3 * K;        // packed weight: q, k, v rows, then a 64-row bias chunk
 constexpr int PACKED_ROWS = QKV_ROWS + CHUNK;
-constexpr int CPITCH = CHUNK + 8;      // staging pitch [row][col] (bf16)
-constexpr int TPITCH = ROWS + 8;       // staging pitch [col][row] (bf16)
-static_assert(CHUNK * TPITCH <= ROWS * CPITCH, "v^T staging must fit the q/k staging area");
+
+// grid_project, one wavefront per unit of 32 attention positions t0 .. t0 + 31 of one batch
+// row b (t0 a multiple of 32, t up to npad so the pad rows and columns come out as zeros),
+// the q, k, v and bias weight rows resident in LDS (rowstep.h layout), the next unit's rows
+// loaded while this one is computed, no barriers after the weights are in. Row m of row tile
+// rt is position t0 + 16 rt + m.
+//   q, k:  out^T = W x^T with W's rows permuted inside each 32-channel head (tile 2s + p, row
+//          r = channel 32 s + 8 (r / 4) + 4 p + r % 4), so the lane holding rows 4 g .. of
+//          both tiles of head s has its channels 32 s + 8 g .. + 7: one 16-byte store;
+//   v^T:   out = x W^T, whose lane (channel, g) holds keys 4 g + e (tile 0) and 16 + 4 g + e
+//          (tile 1): exactly the 8 keys of positions t0 + 8 g .. + 7 of the permuted layout;
+//   bias:  out = x W^T, 4 consecutive keys per lane (starting node) or one value per
+//          (query t, key b) (ending node).
+constexpr int W_ROWS = QKV_ROWS + 16;  // q, k, v, then one tile of bias rows (heads <= 16)
 
 template <typename TIN>
-__global__ __launch_bounds__(256, 2) void grid_project_kernel(GridProjectArgs a) {
-  __shared__ bf16 lds_a[A_ELEMS];                   // A tile, later two B buffers
-  __shared__ bf16 stage[ROWS * CPITCH];             // [128][72] (q, k) or [64][136] (v^T)
-  auto bbuf = [&](int i) -> bf16 * { return lds_a + (i & 1) * B_ELEMS; };
+__global__ __launch_bounds__(512, 1) void grid_project_kernel(GridProjectArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 w_lds[W_ROWS * K];
+  __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
+  for (int i = threadIdx.x; i < W_ROWS * 16; i += blockDim.x) {
+    const int r = i >> 4, c = i & 15;               // LDS row, 16-byte chunk
+    int src = r;
+    if (r < 2 * K) {                                // q, k: permuted inside each head
+      const int blk = r / K, rr = r % K, t = rr / 16, e = rr % 16;
+      src = blk * K + 32 * (t / 2) + 8 * (e / 4) + 4 * (t % 2) + (e % 4);
+    }
+    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) =
+        *reinterpret_cast<const bf16x8 *>(a.w_packed + int64_t(src) * K + c * 8);
+  }
+  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
+  __syncthreads();
 
-  const int n = a.n, H = a.heads;
-  const int ppb = (n + ROWS - 1) / ROWS;            // panels per batch row
-  const int b = blockIdx.x / ppb, t0 = (blockIdx.x % ppb) * ROWS;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
+  const int n = a.n, H = a.heads, npad = a.npad, upr = npad / 32;
+  const int units = n * upr;
+  const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+  const int waves = int(gridDim.x) * int(blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
   // Pair row of attention position (b, t): b*n + t (starting node) or t*n + b (ending node).
-  auto row_of = [&](int t) -> int64_t { return a.transpose ? int64_t(t) * n + b : int64_t(b) * n + t; };
-
-  ln_panel<TIN>([&](int r) -> const TIN * { return (t0 + r < n) ? z + row_of(t0 + r) * K : nullptr; },
-                a.ln_w, a.ln_b, a.eps, lds_a);
-  __syncthreads();
-  AFrags af;
-  load_a_frags(lds_a, wm, af);
-  BStage st;
-  fetch_b(a.w_packed, 0, PACKED_ROWS, st);
-  __syncthreads();
-  stash_b(st, bbuf(0));
-  __syncthreads();
-
-  const int chunks = PACKED_ROWS / CHUNK;           // 2 q, 2 k, 2 v, 1 bias
-  for (int j = 0; j < chunks; ++j) {
-    if (j + 1 < chunks) fetch_b(a.w_packed, (j + 1) * CHUNK, PACKED_ROWS, st);
-    f32x4 acc[4][2];
-    zero(acc);
-    mma_chunk(af, bbuf(j), wn, acc);
-    const int kind = j / 2;                         // 0 q, 1 k, 2 v, 3 bias
-    if (kind == 3) {
-      // Bias: column h < H of this chunk; bias[h][i][j] for pair (i, j) = (b, t) or (t, b).
-      // The pad columns j in [n, npad) are written as zeros (the attention kernel adds its
-      // mask to them, so they must be finite): by the panels with t >= n when j = t, by the
-      // panels of the last batch row when j = b.
-      if (wn == 0 && col < H) {
+  auto pos_of = [&](int b, int t) -> int64_t { return a.transpose ? int64_t(t) * n + b : int64_t(b) * n + t; };
+  struct Unit {
+    rowstep::Raw4<TIN> z[2][8];
+  };
+  auto fetch = [&](int u, Unit &w) {
+    const int b = u / upr, t0 = (u - b * upr) * 32;
 #pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
+    for (int rt = 0; rt < 2; ++rt) {
+      const int t = t0 + 16 * rt + m;
+      rowstep::load_k<TIN>(z + pos_of(b, t < n ? t : n - 1) * K, w.z[rt]);
+    }
+  };
+  int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
+  Unit cur;
+  if (u < units) fetch(u, cur);
+  for (; u < units; u += waves) {
+    Unit next;
+    if (u + waves < units) fetch(u + waves, next);
+    bf16x8 xa[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float v[32];
+      rowstep::k_to_float(cur.z[rt], v);
+      rowstep::ln_k(v, lnw, lnb, a.eps, xa[rt]);
+    }
+    const int b = u / upr, t0 = (u - b * upr) * 32;
+
+    // q (rows < n) and k (rows < npad, zero from n on): [b][h][rows][32].
+#pragma unroll
+    for (int blk = 0; blk < 2; ++blk) {
+      const bf16 *wb = w_lds + blk * K * K;
+      const float scale = blk == 0 ? a.qscale : 1.0f;
+      const int rows = blk == 0 ? n : npad;
+      bf16 *dst_base = blk == 0 ? a.q : a.k;
+#pragma unroll 1
+      for (int s = 0; s < H; ++s) {
+        f32x4 acc[2][2];
+#pragma unroll
+        for (int p = 0; p < 2; ++p)
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) acc[p][rt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+          for (int p = 0; p < 2; ++p) {
+            const bf16x8 wf = rowstep::weight_frag(wb, 2 * s + p, ks);
+#pragma unroll
+            for (int rt = 0; rt < 2; ++rt) acc[p][rt] = mfma16(wf, xa[rt][ks], acc[p][rt]);
+          }
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const int t = t0 + 16 * rt + m;
+          if (t >= rows) continue;
+          bf16x8 v;
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
-            const int t = t0 + wm * 64 + mt * 16 + grp * 4 + e;
-            if (t >= n) {
-              if (!a.transpose && t < a.npad) a.bias[(int64_t(col) * n + b) * a.npad + t] = 0.0f;
-              continue;
-            }
-            const int64_t qi = a.transpose ? t : b, kj = a.transpose ? b : t;
-            float *row = a.bias + (int64_t(col) * n + qi) * a.npad;
-            row[kj] = acc[mt][0][e] * kLog2e;
-            if (a.transpose && b == n - 1)
-              for (int j = n; j < a.npad; ++j) row[j] = 0.0f;
+            v[e] = bf16(acc[0][rt][e] * scale);
+            v[4 + e] = bf16(acc[1][rt][e] * scale);
           }
-      }
-    } else if (kind < 2) {
-      // q or k: stage [row t][64 cols] then 16-byte rows of [b][h][t][32].
-      const float scale = kind == 0 ? a.qscale : 1.0f;
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt)
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            stage[(wm * 64 + mt * 16 + grp * 4 + e) * CPITCH + wn * 32 + nt * 16 + col] =
-                bf16(acc[mt][nt][e] * scale);
-      __syncthreads();
-      // q rows: [b][h][n][32]; k rows: [b][h][npad][32], zero for n <= t < npad (the
-      // attention kernel loads whole 64-key blocks of k without bounds).
-      bf16 *dst = kind == 0 ? a.q : a.k;
-      const int rows = kind == 0 ? n : a.npad;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int idx = tid + i * 256;              // 128 rows x 8 chunks of 8
-        const int r = idx >> 3, c = (idx & 7) * 8;
-        const int t = t0 + r;
-        if (t >= rows) continue;
-        const int h = (j & 1) * 2 + c / HD;
-        bf16x8 v = *reinterpret_cast<const bf16x8 *>(&stage[r * CPITCH + c]);
-        if (t >= n) v = bf16x8{};
-        *reinterpret_cast<bf16x8 *>(dst + ((int64_t(b) * H + h) * rows + t) * HD + (c % HD)) = v;
-      }
-    } else {
-      // v: stage transposed [64 cols][128 rows] then [b][h][d][npad] rows, zero beyond n.
-      // Inside every run of 32 keys, position 8g + j holds key 4g + j (j < 4) or
-      // 16 + 4g + (j - 4) (j >= 4): the key order of the attention kernel's P^T fragment,
-      // so that one 16-byte LDS read there yields a whole V^T fragment.
-#pragma unroll
-      for (int mt = 0; mt < 4; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < 2; ++nt) {
-          bf16x4 v;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = bf16(acc[mt][nt][e]);
-          *reinterpret_cast<bf16x4 *>(&stage[(wn * 32 + nt * 16 + col) * TPITCH + wm * 64 + mt * 16 + grp * 4]) = v;
+          if (t >= n) v = bf16x8{};
+          *reinterpret_cast<bf16x8 *>(dst_base + ((int64_t(b) * H + s) * rows + t) * HD + 8 * g) = v;
         }
-      __syncthreads();
+      }
+    }
+
+    // v^T: [b][h][d][npad], keys permuted in runs of 32 (zero from n on).
+    {
+      const bf16 *wv = w_lds + 2 * K * K;
+#pragma unroll 1
+      for (int tile = 0; tile < K / 16; ++tile) {
+        f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int idx = tid + i * 256;              // 64 cols x 16 chunks of 8 rows
-        const int c = idx >> 4, rc = (idx & 15) * 8;    // positions rc .. rc+7 of the panel
-        const int t = t0 + rc;
-        if (t >= a.npad) continue;
-        const int h = (j & 1) * 2 + c / HD, d = c % HD;
-        const int key0 = (rc & ~31) + ((rc & 31) >> 1);   // panel-relative: 4g, and 16 + 4g
-        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&stage[c * TPITCH + key0]);
-        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&stage[c * TPITCH + key0 + 16]);
+        for (int ks = 0; ks < 4; ++ks) {
+          const bf16x8 wf = rowstep::weight_frag(wv, tile, ks);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) acc[rt] = mfma16(xa[rt][ks], wf, acc[rt]);
+        }
+        const int c = tile * 16 + m, h = c / HD, d = c % HD;
         bf16x8 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          v[e] = t0 + key0 + e < n ? lo[e] : bf16(0.0f);
-          v[4 + e] = t0 + key0 + 16 + e < n ? hi[e] : bf16(0.0f);
+          v[e] = t0 + 4 * g + e < n ? bf16(acc[0][e]) : bf16(0.0f);
+          v[4 + e] = t0 + 16 + 4 * g + e < n ? bf16(acc[1][e]) : bf16(0.0f);
         }
-        *reinterpret_cast<bf16x8 *>(a.vt + ((int64_t(b) * H + h) * HD + d) * a.npad + t) = v;
+        *reinterpret_cast<bf16x8 *>(a.vt + ((int64_t(b) * H + h) * HD + d) * npad + t0 + 8 * g) = v;
       }
     }
-    if (j + 1 < chunks) stash_b(st, bbuf(j + 1));
-    __syncthreads();
+
+    // Bias, from the un-transposed pair: bias[h][i][j] for pair (i, j) = (b, t) starting node,
+    // (t, b) ending node; the pad columns j in [n, npad) are zeros.
+    {
+      const bf16 *wbias = w_lds + QKV_ROWS * K;
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 wf = rowstep::weight_frag(wbias, 0, ks);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) acc[rt] = mfma16(xa[rt][ks], wf, acc[rt]);
+      }
+      if (m < H) {
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          const int tb = t0 + 16 * rt + 4 * g;        // keys / queries tb .. tb + 3
+          if (!a.transpose) {
+            float4 v;
+            v.x = tb + 0 < n ? acc[rt][0] * kLog2e : 0.f;
+            v.y = tb + 1 < n ? acc[rt][1] * kLog2e : 0.f;
+            v.z = tb + 2 < n ? acc[rt][2] * kLog2e : 0.f;
+            v.w = tb + 3 < n ? acc[rt][3] * kLog2e : 0.f;
+            *reinterpret_cast<float4 *>(a.bias + (int64_t(m) * n + b) * npad + tb) = v;
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int t = tb + e;
+              if (t >= n) continue;
+              float *row = a.bias + (int64_t(m) * n + t) * npad;
+              row[b] = acc[rt][e] * kLog2e;
+              if (b == n - 1)
+                for (int j = n; j < npad; ++j) row[j] = 0.0f;
+            }
+          }
+        }
+      }
+    }
+    cur = next;
   }
 }
 
@@ -300,12 +341,17 @@ int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb,
 }
 
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {
-  const int64_t panels = int64_t(a.n) * ceil_div(a.n, ROWS);
+  if (a.npad % 64 != 0 || a.npad < a.n || a.heads > 16 || a.heads * HD != K)
+    return fail(XFH_EINVAL, "grid_project: npad must be a multiple of 64 >= n, heads * 32 == 128");
+  const int64_t units = int64_t(a.n) * (a.npad / 32);
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
   KernelTimer timer("grid_project", s);
   if (pair_dtype == XFH_BF16)
-    grid_project_kernel<bf16><<<dim3(panels), 256, 0, s>>>(a);
+    grid_project_kernel<bf16><<<grid, 512, 0, s>>>(a);
   else
-    grid_project_kernel<float><<<dim3(panels), 256, 0, s>>>(a);
+    grid_project_kernel<float><<<grid, 512, 0, s>>>(a);
   return check_launch("grid_project");
 }
 
