@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 4
+#define XFH_ABI_VERSION 5
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -140,6 +140,18 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
  * 258-271) feed the attention biases of a whole super-block, which it converts once
  * instead of once per block. */
 int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides,
+                            void *packed, void *stream);
+
+/* Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' straight into the packed bias layout
+ * of xfh_attention_bias_pack: packed[h][i][j] fp32 = log2(e) * (LN(pair[i][j]) . w[h]) for
+ * j < n, 0 for n <= j < align64(n); pair contiguous [n, n, c] (f32/bf16, c = 128), LayerNorm
+ * affine ln_w/ln_b (fp32, may be null), w bf16 [heads][c] (heads <= 384), computed in bf16
+ * with fp32 accumulation. Each block of heads is then an XFH_BIAS_PACKED bias. Replaces the
+ * pair-logits path of PairformerBlock's single-track attention
+ * (xfold/nn/pairformer.py:103-106) and of DiffusionTransformer
+ * (xfold/nn/diffusion_transformer.py:258-271, all super-blocks' projections stacked). */
+int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t c, const float *ln_w,
+                            const float *ln_b, float eps, const void *w, int w_dtype, int64_t heads,
                             void *packed, void *stream);
 
 /* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).

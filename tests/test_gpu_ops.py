@@ -176,6 +176,25 @@ def test_gated_linear_unit(device, m, k, f, dtype):
 
 # ---------------------------------------------------------------------------- attention
 
+@pytest.mark.parametrize("n,heads", [(70, 16), (33, 20), (128, 384)])
+@pytest.mark.parametrize("pair_dtype", [torch.float32, torch.bfloat16])
+def test_pair_attention_bias(device, n, heads, pair_dtype):
+    """Linear(LayerNorm(pair)) rearranged to [h, i, j], times log2(e), in the packed layout
+    with zero pad columns (xfold/nn/pairformer.py:103-106)."""
+    announce("pair_attention_bias", n, heads, pair_dtype)
+    g = torch.Generator().manual_seed(n + heads)
+    pair = (torch.randn(n, n, 128, generator=g) * 2 + 0.5).to(pair_dtype)
+    ln_w, ln_b = 1 + 0.1 * torch.randn(128, generator=g), 0.1 * torch.randn(128, generator=g)
+    w = (torch.randn(heads, 128, generator=g) / math.sqrt(128)).bfloat16()
+    want = F.layer_norm(pair.float(), (128,), ln_w, ln_b, 1e-5) @ w.float().T
+    want = want.permute(2, 0, 1) * math.log2(math.e)
+    got = ops.pair_attention_bias(pair.to(device), ln_w.to(device), ln_b.to(device), 1e-5, w.to(device))
+    npad = (n + 63) // 64 * 64
+    assert got.shape == (heads, n, npad)
+    assert bool((got[..., n:] == 0).all())
+    assert_parity_bf16(got[..., :n], want, "pair_attention_bias")
+
+
 @pytest.mark.parametrize("d", [32, 48, 64])
 @pytest.mark.parametrize("head_minor", [True, False])
 def test_attention_packed_bias(device, d, head_minor):

@@ -341,6 +341,24 @@ int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, c
   return attention_bias_pack(bias, dtype, shape, strides, packed, as_stream(stream));
 }
 
+int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t c, const float *ln_w,
+                            const float *ln_b, float eps, const void *w, int w_dtype, int64_t heads,
+                            void *packed, void *stream) {
+  XFH_REQUIRE(float_dtype(pair_dtype), "pair_attention_bias: pair dtype must be f32/bf16");
+  XFH_REQUIRE(w_dtype == XFH_BF16, "pair_attention_bias: the weight must be bf16");
+  XFH_REQUIRE(c == 128, "pair_attention_bias: 128 pair channels");
+  XFH_REQUIRE(heads > 0 && heads <= pair_bias_max_heads(), "pair_attention_bias: 1..384 heads");
+  XFH_REQUIRE(n >= 0 && n <= grid_attention_max_n(), "pair_attention_bias: more keys than the attention kernel takes");
+  XFH_REQUIRE(eps >= 0.f, "pair_attention_bias: eps must be nonnegative");
+  if (n == 0) return XFH_OK;
+  XFH_REQUIRE(pair && w && packed, "pair_attention_bias: null tensor");
+  PairBiasArgs a;
+  a.pair = pair; a.ln_w = ln_w; a.ln_b = ln_b; a.eps = eps;
+  a.w = static_cast<const bf16 *>(w); a.packed = static_cast<float *>(packed);
+  a.n = int(n); a.npad = int(align_up(n, 64)); a.heads = int(heads);
+  return pair_bias(a, pair_dtype, as_stream(stream));
+}
+
 int64_t xfh_triangle_multiplication_workspace_size(int64_t n, int64_t c, int dtype) {
   if (n < 0 || c < 0 || !float_dtype(dtype)) return -1;
   Carver cv(nullptr, 0);

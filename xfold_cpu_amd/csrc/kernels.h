@@ -54,6 +54,17 @@ bool mha_supported(const AttentionArgs &a, int dtype);
 int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStream_t s);
 int attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides, void *packed,
                         hipStream_t s);
+// Linear(LayerNorm(pair)) straight into the packed attention-bias layout (pair_bias.hip).
+struct PairBiasArgs {
+  const void *pair;          // [n][n][128]
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w;             // [heads][128]
+  float *packed;             // [heads][n][npad]
+  int n, npad, heads;
+};
+int pair_bias_max_heads();
+int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s);
 
 // Triangle (grid) attention, bf16, head dim 32 (grid_attention.hip).
 // Layouts (D = padded head dim, 32 or 64): q [B][H][Nq][D] pre-scaled by d^-0.5 * log2(e);

@@ -1,0 +1,118 @@
+// Pair-logits attention biases straight from the pair tensor (bf16 compute, c = 128):
+//   packed[h][i][j] = log2(e) * sum_k LN(z[i][j])[k] * W[h][k]   (j < n; 0 for n <= j < npad)
+// i.e. Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' into the attention kernel's bias
+// layout (grid_attention.hip: [H][Nq][Npad] fp32 times log2(e)), for
+//   - PairformerBlock's single-track attention bias (xfold/nn/pairformer.py:103-106), and
+//   - DiffusionTransformer's pair logits (xfold/nn/diffusion_transformer.py:258-271), all
+//     super-blocks' projections stacked into one weight, so the pair is read once.
+//
+// One wavefront per unit of 32 pair positions (i, j0 .. j0 + 31) (j0 a multiple of 32, j up
+// to npad so the pad columns come out as zeros), the projection weight resident in LDS
+// (rowstep.h layout), the next unit's rows loaded while this one is computed, no barriers
+// after the weight is in. Row m of row tile rt is position j0 + 16 rt + m, so out = x W^T
+// leaves 4 consecutive keys of one head in a lane: one 16-byte store per head and tile.
+#include <algorithm>
+
+#include "common.h"
+#include "kernels.h"
+#include "rowstep.h"
+
+namespace xfh {
+
+namespace {
+
+constexpr int K = rowstep::C;          // pair channels
+constexpr int MAX_HEADS = 384;         // LDS rows of the projection weight
+constexpr float kLog2eF = 1.4426950408889634f;
+
+template <typename TIN>
+__global__ __launch_bounds__(512, 1) void pair_bias_kernel(PairBiasArgs a) {
+  __shared__ __attribute__((aligned(16))) bf16 w_lds[MAX_HEADS * K];
+  __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
+  const int tiles = (a.heads + 15) / 16;
+  for (int i = threadIdx.x; i < tiles * 16 * 16; i += blockDim.x) {
+    const int r = i >> 4, c = i & 15;               // LDS row, 16-byte chunk
+    bf16x8 v = {};
+    if (r < a.heads) v = *reinterpret_cast<const bf16x8 *>(a.w + int64_t(r) * K + c * 8);
+    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) = v;
+  }
+  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
+  __syncthreads();
+
+  const int n = a.n, npad = a.npad, upr = npad / 32;
+  const int units = n * upr;
+  const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
+  const int waves = int(gridDim.x) * int(blockDim.x >> 6);
+  const TIN *z = static_cast<const TIN *>(a.pair);
+  struct Unit {
+    rowstep::Raw4<TIN> z[2][8];
+  };
+  auto fetch = [&](int u, Unit &w) {
+    const int i = u / upr, j0 = (u - i * upr) * 32;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const int j = j0 + 16 * rt + m;
+      rowstep::load_k<TIN>(z + (int64_t(i) * n + (j < n ? j : n - 1)) * K, w.z[rt]);
+    }
+  };
+  int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
+  Unit cur;
+  if (u < units) fetch(u, cur);
+  for (; u < units; u += waves) {
+    Unit next;
+    if (u + waves < units) fetch(u + waves, next);
+    bf16x8 xa[2][4];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float v[32];
+      rowstep::k_to_float(cur.z[rt], v);
+      rowstep::ln_k(v, lnw, lnb, a.eps, xa[rt]);
+    }
+    const int i = u / upr, j0 = (u - i * upr) * 32;
+#pragma unroll 1
+    for (int t = 0; t < tiles; ++t) {
+      f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 wf = rowstep::weight_frag(w_lds, t, ks);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) acc[rt] = mfma16(xa[rt][ks], wf, acc[rt]);
+      }
+      const int h = 16 * t + m;
+      if (h >= a.heads) continue;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt) {
+        const int jb = j0 + 16 * rt + 4 * g;        // keys jb .. jb + 3
+        float4 v;
+        v.x = jb + 0 < n ? acc[rt][0] * kLog2eF : 0.f;
+        v.y = jb + 1 < n ? acc[rt][1] * kLog2eF : 0.f;
+        v.z = jb + 2 < n ? acc[rt][2] * kLog2eF : 0.f;
+        v.w = jb + 3 < n ? acc[rt][3] * kLog2eF : 0.f;
+        *reinterpret_cast<float4 *>(a.packed + (int64_t(h) * n + i) * npad + jb) = v;
+      }
+    }
+    cur = next;
+  }
+}
+
+}  // namespace
+
+int pair_bias_max_heads() { return MAX_HEADS; }
+
+int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s) {
+  if (a.heads <= 0 || a.heads > MAX_HEADS || a.npad % 64 != 0 || a.npad < a.n)
+    return fail(XFH_EINVAL, "pair_attention_bias: 1..384 heads, npad a multiple of 64 >= n");
+  const int64_t units = int64_t(a.n) * (a.npad / 32);
+  if (units == 0) return XFH_OK;
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
+  KernelTimer timer("pair_bias", s);
+  if (pair_dtype == XFH_BF16)
+    pair_bias_kernel<bf16><<<grid, 512, 0, s>>>(a);
+  else
+    pair_bias_kernel<float><<<grid, 512, 0, s>>>(a);
+  return check_launch("pair_bias");
+}
+
+}  // namespace xfh

@@ -163,6 +163,24 @@ def attention_bias_pack(bias: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pair_attention_bias(pair: torch.Tensor, ln_w: Optional[torch.Tensor], ln_b: Optional[torch.Tensor],
+                        eps: float, weight: torch.Tensor, owner: Optional[torch.nn.Module] = None) -> torch.Tensor:
+    """Linear(LayerNorm(pair)) as attention biases, [heads, N, align64(N)] fp32 in the packed
+    layout (one :class:`PackedBias` per block of heads); weight [heads, 128] in bf16."""
+    n = pair.shape[0]
+    if pair.dim() != 3 or pair.shape[1] != n or weight.dtype != torch.bfloat16:
+        raise ValueError("pair_attention_bias: pair [N, N, C] and a bf16 weight")
+    pair_c = pair.contiguous()
+    heads = weight.shape[0]
+    out = torch.empty((heads, n, (n + 63) // 64 * 64), dtype=torch.float32, device=pair.device)
+    w = _fp32(ln_w, owner, "ln_weight")
+    b = _fp32(ln_b, owner, "ln_bias")
+    nh.call("xfh_pair_attention_bias", nh.ptr(pair_c), nh.dtype_code(pair.dtype), n, pair.shape[2],
+            nh.ptr(w), nh.ptr(b), float(eps), nh.ptr(weight.contiguous()), nh.BF16, heads, nh.ptr(out),
+            nh.stream_of(pair.device))
+    return out
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
               bias: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:

@@ -220,14 +220,30 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         raise ValueError("DiffusionTransformer (hip) updates act in place; pass a contiguous tensor")
     dtype = nh.compute_dtype(act, module.pair_logits_projection[0].weight)
     ln = module.pair_input_layer_norm
-    pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
-                              out_dtype=dtype, owner=ln)
     heads, size = module.num_head, module.super_block_size
     conds = _block_conditioning(module, single_cond, dtype, act.dtype)
     if mask is not None and mask.dtype not in (torch.bool, torch.uint8):
         mask = mask.to(torch.bool)      # once, not per block (xfold/fastnn/attention.py:57-61)
-    packed_bias = dtype == torch.bfloat16 and module.self_attention[0].num_head == heads and \
-        act.shape[-1] // heads <= 64
+    n_blocks = module.num_super_blocks * size
+    if dtype == torch.bfloat16 and act.shape[-1] // heads <= 64 and pair_cond.shape[-1] == 128 and \
+            n_blocks * heads <= 384 and tuple(ln.normalized_shape) == (128,):
+        # Every super-block's pair logits in one pass over pair_cond, straight into the
+        # attention kernel's bias layout; block b reads heads b*H .. b*H + H - 1.
+        projs = [module.pair_logits_projection[s].weight for s in range(module.num_super_blocks)]
+        w_all = nh.derived_weight(module, f"pair_logits:{dtype}", projs,
+                                  lambda *ws: torch.cat([w.detach() for w in ws], dim=0).to(dtype).contiguous())
+        packed = ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln)
+        for index in range(n_blocks):
+            att_cond, tr_cond = (None, None) if conds is None else conds[index]
+            bias = ops.PackedBias(packed[index * heads:(index + 1) * heads])
+            self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
+                               accumulate_into=act, _cond=att_cond)
+            diffusion_transition_hip(module.transition_block[index], act, single_cond,
+                                     accumulate_into=act, _cond=tr_cond)
+        return act
+    pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
+                              out_dtype=dtype, owner=ln)
+    packed_bias = dtype == torch.bfloat16 and act.shape[-1] // heads <= 64
     for s in range(module.num_super_blocks):
         weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
         logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]
