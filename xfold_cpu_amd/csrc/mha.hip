@@ -27,6 +27,7 @@ struct MhaPrep {
   bf16 *q, *k, *vt;
   float *bias;
   uint64_t *words;
+  bool vec_qk;               // q and k rows hold whole 16-byte chunks (D, strides % 8, aligned)
 };
 
 template <typename T> __device__ __forceinline__ float ld(const void *p, int64_t i) {
@@ -46,10 +47,17 @@ __global__ void mha_prepare_kernel(MhaPrep p, int part) {
       const bf16 *src = static_cast<const bf16 *>(a.q) + b * a.qs[0] + h * a.qs[1] + n * a.qs[2];
       const float s = a.scale * kLog2eF;
       bf16x8 v;
+      if (p.vec_qk) {                               // one 16-byte load per chunk
+        bf16x8 x = {};
+        if (c * 8 < a.D) x = *reinterpret_cast<const bf16x8 *>(src + c * 8);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = c * 8 + e;
-        v[e] = bf16(d < a.D ? static_cast<float>(src[d]) * s : 0.f);
+        for (int e = 0; e < 8; ++e) v[e] = bf16(static_cast<float>(x[e]) * s);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int d = c * 8 + e;
+          v[e] = bf16(d < a.D ? static_cast<float>(src[d]) * s : 0.f);
+        }
       }
       *reinterpret_cast<bf16x8 *>(p.q + row * D + c * 8) = v;
       return;
@@ -60,11 +68,15 @@ __global__ void mha_prepare_kernel(MhaPrep p, int part) {
       const int c = int(idx % dc);
       const int64_t row = idx / dc, key = row % p.npad, bh = row / p.npad, h = bh % a.H, b = bh / a.H;
       const bf16 *src = static_cast<const bf16 *>(a.k) + b * a.ks[0] + h * a.ks[1] + key * a.ks[2];
-      bf16x8 v;
+      bf16x8 v = {};
+      if (p.vec_qk) {
+        if (key < a.K && c * 8 < a.D) v = *reinterpret_cast<const bf16x8 *>(src + c * 8);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int d = c * 8 + e;
-        v[e] = (key < a.K && d < a.D) ? src[d] : bf16(0.f);
+        for (int e = 0; e < 8; ++e) {
+          const int d = c * 8 + e;
+          v[e] = (key < a.K && d < a.D) ? src[d] : bf16(0.f);
+        }
       }
       *reinterpret_cast<bf16x8 *>(p.k + row * D + c * 8) = v;
       return;
@@ -191,6 +203,9 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
   p.vt = static_cast<bf16 *>(cv.take(pl.v_bytes));
   p.bias = static_cast<float *>(cv.take(pl.bias_bytes));
   p.words = static_cast<uint64_t *>(cv.take(pl.word_bytes));
+  p.vec_qk = a.D % 8 == 0 && a.qs[0] % 8 == 0 && a.qs[1] % 8 == 0 && a.qs[2] % 8 == 0 && a.ks[0] % 8 == 0 &&
+             a.ks[1] % 8 == 0 && a.ks[2] % 8 == 0 && reinterpret_cast<uintptr_t>(a.q) % 16 == 0 &&
+             reinterpret_cast<uintptr_t>(a.k) % 16 == 0;
   const int dc = pl.D / 8;
   const int64_t work[5] = {a.B * a.H * a.Q * dc, a.B * a.H * pl.npad * dc, a.B * a.H * (pl.npad / 8) * pl.D,
                            a.H * a.Q * (pl.npad / 4), pl.mask_rows * pl.nblk * 64};
