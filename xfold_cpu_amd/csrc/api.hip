@@ -120,7 +120,7 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
 struct GridPlan {
   void *normed, *bias, *qkv, *attn;
   // fast bf16 path (c = 128, 4 heads x 32)
-  void *qh, *kh, *vt, *packed;
+  void *qh, *kh, *vt;
   float *bias_t;
   uint64_t *maskbits;
 };
@@ -134,7 +134,6 @@ static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t
   std::memset(&p, 0, sizeof(p));
   if (grid_fast_path(n, c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
-    p.packed = cv.take(grid_packed_rows() * c * es);
     p.qh = cv.take(plane * c * es);
     p.kh = cv.take(n * c * npad * es);
     p.vt = cv.take(n * c * npad * es);
@@ -466,12 +465,12 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   const int64_t row_b = transpose ? 1 : n, row_t = transpose ? n : 1;
   if (grid_fast_path(n, c, heads, dtype)) {
     const int64_t npad = grid_attention_pad(n);
-    XFH_TRY(grid_prepare(q_w, k_w, v_w, bias_w, int(c), int(heads), p.packed, mask, mask_dtype, n,
-                         npad / 64, p.maskbits, s));
     GridProjectArgs pa;
     pa.pair = pair; pa.n = int(n); pa.heads = int(heads); pa.transpose = transpose;
     pa.ln_w = norm_w; pa.ln_b = norm_b; pa.eps = eps;
-    pa.w_packed = static_cast<const bf16 *>(p.packed);
+    pa.wq = static_cast<const bf16 *>(q_w); pa.wk = static_cast<const bf16 *>(k_w);
+    pa.wv = static_cast<const bf16 *>(v_w); pa.wb = static_cast<const bf16 *>(bias_w);
+    pa.mask = mask; pa.mask_dtype = mask_dtype; pa.maskbits = p.maskbits;
     pa.qscale = kLog2e / std::sqrt(float(dh));
     pa.q = static_cast<bf16 *>(p.qh); pa.k = static_cast<bf16 *>(p.kh); pa.vt = static_cast<bf16 *>(p.vt);
     pa.bias = p.bias_t; pa.npad = int(npad);

@@ -1,14 +1,13 @@
 // Fused projection and output kernels around the triangle-attention core (bf16 compute,
 // c = 128, 4 heads x 32), following GridSelfAttention.forward (xfold/nn/attention.py:80-105):
 //
-//   grid_project: LN(z) -> GEMMs over the packed [q | k | v | bias] weight (resident in
-//       LDS) -> q scaled by d^-0.5 * log2(e), k (rows up to npad, zero beyond n), v^T (zero
-//       beyond n, keys permuted in runs of 32) and the fp32 pair bias (times log2(e)), each
-//       written straight into the attention kernel's layout (grid_attention.hip). The bias
-//       comes from the un-transposed pair in both directions.
+//   grid_project: LN(z) -> GEMMs over the q, k, v and bias weights (resident in LDS) -> q
+//       scaled by d^-0.5 * log2(e), k (rows up to npad, zero beyond n), v^T (zero
+//       beyond n, keys permuted in runs of 32), the fp32 pair bias (times log2(e)) and the
+//       kept-key words, each written straight into the attention kernel's layout
+//       (grid_attention.hip). The bias comes from the un-transposed pair in both directions.
 //   grid_output: gate = sigmoid(LN(z) Wgating^T) (recomputed: z is read here anyway for
 //       the residual) -> (gate * o) Wout^T -> z += update (or update stored).
-//   grid_prepare: the packed weight and the attention kernel's kept-key words, one launch.
 #include <algorithm>
 
 #include "common.h"
@@ -23,8 +22,7 @@ namespace {
 using namespace panel;
 
 constexpr int HD = 32;                 // head dim
-constexpr int QKV_ROWS = 3 * K;        // packed weight: q, k, v rows, then a 64-row bias chunk
-constexpr int PACKED_ROWS = QKV_ROWS + CHUNK;
+constexpr int QKV_ROWS = 3 * K;        // q, k, v weight rows in LDS, then the bias rows
 
 // grid_project, one wavefront per unit of 32 attention positions t0 .. t0 + 31 of one batch
 // row b (t0 a multiple of 32, t up to npad so the pad rows and columns come out as zeros),
@@ -46,21 +44,38 @@ __global__ __launch_bounds__(512, 1) void grid_project_kernel(GridProjectArgs a)
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
   for (int i = threadIdx.x; i < W_ROWS * 16; i += blockDim.x) {
     const int r = i >> 4, c = i & 15;               // LDS row, 16-byte chunk
-    int src = r;
-    if (r < 2 * K) {                                // q, k: permuted inside each head
-      const int blk = r / K, rr = r % K, t = rr / 16, e = rr % 16;
-      src = blk * K + 32 * (t / 2) + 8 * (e / 4) + 4 * (t % 2) + (e % 4);
+    const int blk = r / K, rr = r % K;              // q, k, v, bias
+    const bf16 *src = nullptr;
+    if (blk < 2) {                                  // q, k: rows permuted inside each head
+      const int t = rr / 16, e = rr % 16;
+      src = (blk == 0 ? a.wq : a.wk) + (32 * (t / 2) + 8 * (e / 4) + 4 * (t % 2) + (e % 4)) * K;
+    } else if (blk == 2) {
+      src = a.wv + rr * K;
+    } else if (rr < a.heads) {
+      src = a.wb + rr * K;
     }
-    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) =
-        *reinterpret_cast<const bf16x8 *>(a.w_packed + int64_t(src) * K + c * 8);
+    bf16x8 v = {};
+    if (src) v = *reinterpret_cast<const bf16x8 *>(src + c * 8);
+    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) = v;
   }
   rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
-  __syncthreads();
 
   const int n = a.n, H = a.heads, npad = a.npad, upr = npad / 32;
   const int units = n * upr;
   const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
   const int waves = int(gridDim.x) * int(blockDim.x >> 6);
+  // The attention kernel's kept-key words: word w of row b has bit i set iff key 64 w + i < n
+  // is kept (mask[b*n + key] != 0); one wavefront ballot per word.
+  {
+    const int nblk = npad / 64;
+    for (int wd = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6); wd < n * nblk; wd += waves) {
+      const int b = wd / nblk, key = (wd - b * nblk) * 64 + lane;
+      const bool keep = key < n && (!a.mask || load_any(a.mask, a.mask_dtype, int64_t(b) * n + key) != 0.f);
+      const uint64_t ballot = __ballot(keep);
+      if (lane == 0) a.maskbits[wd] = ballot;
+    }
+  }
+  __syncthreads();
   const TIN *z = static_cast<const TIN *>(a.pair);
   // Pair row of attention position (b, t): b*n + t (starting node) or t*n + b (ending node).
   auto pos_of = [&](int b, int t) -> int64_t { return a.transpose ? int64_t(t) * n + b : int64_t(b) * n + t; };
@@ -296,49 +311,7 @@ __global__ __launch_bounds__(512, 1) void grid_output_kernel(GridOutputArgs a) {
   }
 }
 
-// Blocks [0, pack_blocks): packed weight [3c + 64][c] (q, k, v, then the bias rows
-// zero-padded to 64), one element per thread. The rest: one wavefront per 64-key word,
-// lane i tests key w*64 + i and the ballot is the word.
-__global__ void grid_prepare_kernel(const bf16 *__restrict__ wq, const bf16 *__restrict__ wk,
-                                    const bf16 *__restrict__ wv, const bf16 *__restrict__ wb, int c,
-                                    int heads, bf16 *__restrict__ packed, int64_t pack_blocks,
-                                    const void *__restrict__ mask, int mask_dtype, int64_t n, int64_t nblk,
-                                    uint64_t *__restrict__ bits) {
-  if (blockIdx.x < pack_blocks) {
-    const int64_t idx = int64_t(blockIdx.x) * 256 + threadIdx.x;
-    if (idx >= int64_t(PACKED_ROWS) * c) return;
-    const int r = int(idx / c), k = int(idx % c);
-    bf16 v = bf16(0.0f);
-    if (r < c) v = wq[int64_t(r) * c + k];
-    else if (r < 2 * c) v = wk[int64_t(r - c) * c + k];
-    else if (r < 3 * c) v = wv[int64_t(r - 2 * c) * c + k];
-    else if (r - 3 * c < heads) v = wb[int64_t(r - 3 * c) * c + k];
-    packed[idx] = v;
-    return;
-  }
-  const int64_t word = (int64_t(blockIdx.x) - pack_blocks) * 4 + (threadIdx.x >> 6);
-  if (word >= n * nblk) return;
-  const int64_t b = word / nblk, w = word % nblk;
-  const int64_t k = w * 64 + (threadIdx.x & 63);
-  const bool keep = k < n && (!mask || load_any(mask, mask_dtype, b * n + k) != 0.f);
-  const uint64_t ballot = __ballot(keep);
-  if ((threadIdx.x & 63) == 0) bits[word] = ballot;
-}
-
 }  // namespace
-
-int64_t grid_packed_rows() { return PACKED_ROWS; }
-
-int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
-                 void *packed, const void *mask, int mask_dtype, int64_t n, int64_t nblk,
-                 uint64_t *bits, hipStream_t s) {
-  const int64_t pack_blocks = ceil_div(int64_t(PACKED_ROWS) * c, 256);
-  const int64_t word_blocks = ceil_div(n * nblk, 4);
-  grid_prepare_kernel<<<dim3(pack_blocks + word_blocks), 256, 0, s>>>(
-      (const bf16 *)wq, (const bf16 *)wk, (const bf16 *)wv, (const bf16 *)wb, c, heads, (bf16 *)packed,
-      pack_blocks, mask, mask_dtype, n, nblk, bits);
-  return check_launch("grid_prepare");
-}
 
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {
   if (a.npad % 64 != 0 || a.npad < a.n || a.heads > 16 || a.heads * HD != K)

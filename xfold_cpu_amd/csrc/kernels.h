@@ -85,7 +85,10 @@ struct GridProjectArgs {
   int n, heads, transpose;
   const float *ln_w, *ln_b;
   float eps;
-  const bf16 *w_packed;      // [3c + 64][c], see grid_prepare
+  const bf16 *wq, *wk, *wv, *wb;  // nn.Linear weights [c][c] (wb: [heads][c])
+  const void *mask;          // [n][n] (key k of row b at b*n + k), or null
+  int mask_dtype;
+  uint64_t *maskbits;        // [n][npad/64] kept-key words for the attention kernel
   float qscale;              // d^-0.5 * log2(e)
   bf16 *q, *k, *vt;
   float *bias;
@@ -100,13 +103,9 @@ struct GridOutputArgs {
   void *out;
   int accumulate, n;
 };
-int64_t grid_packed_rows();
 // One launch: the packed [q | k | v | bias] weight of grid_project and the 64-bit
 // kept-key words of the attention kernel (bit s of word b*nblk + s/64 set iff key s < n of
 // batch row b is kept, mask[b*n + s] != 0).
-int grid_prepare(const void *wq, const void *wk, const void *wv, const void *wb, int c, int heads,
-                 void *packed, const void *mask, int mask_dtype, int64_t n, int64_t nblk,
-                 uint64_t *bits, hipStream_t s);
 int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s);
 int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);
 int64_t grid_attention_pad(int64_t n);
