@@ -18,6 +18,7 @@ struct GemmArgs {
   int64_t ldaux, sAux, aux_rows;
   int M, N, K;
   int epi;                  // XFH_EPI_*
+  int xcd_rows;             // gemm_ring: give each XCD a contiguous run of row-major tiles
   int glu_f;                // GLU output features (GLU launches only)
 };
 
