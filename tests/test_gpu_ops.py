@@ -67,6 +67,22 @@ def test_layer_norm(device, cols, dt_in, dt_out, affine):
         assert_parity(got, want, TOL_FP32, "layer_norm")
 
 
+@pytest.mark.parametrize("dt_in,dt_out", [(torch.float32, torch.float32), (torch.bfloat16, torch.bfloat16),
+                                          (torch.float32, torch.bfloat16)])
+def test_layer_norm_many_rows(device, dt_in, dt_out):
+    """Pair-sized row counts (several rows per lane group), not a multiple of 4 rows."""
+    announce("layer_norm many rows", dt_in, dt_out)
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(70001, 128, generator=g) * 2 - 0.5).to(dt_in)
+    w, b = torch.randn(128, generator=g), torch.randn(128, generator=g)
+    want = F.layer_norm(x.float(), (128,), w, b, 1e-5)
+    got = ops.layer_norm(x.to(device), (128,), w.to(device), b.to(device), 1e-5, out_dtype=dt_out)
+    if dt_out == torch.bfloat16:
+        assert_parity_bf16(got, want, "layer_norm many rows")
+    else:
+        assert_parity(got, want, TOL_FP32, "layer_norm many rows")
+
+
 def test_layer_norm_module_dtype_contract(device):
     ln = fastnn.LayerNorm(128).eval().to(device)
     x = torch.randn(4, 128, device=device, dtype=torch.bfloat16)

@@ -215,6 +215,7 @@ static int dispatch_rows(const void *x, int xd, int64_t rows, int64_t C, const f
 
 int layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, const float *w, const float *b,
                     float eps, void *y, int yd, hipStream_t s) {
+  KernelTimer timer("layer_norm", s);
   return dispatch_rows<0, float>(x, xd, rows, C, w, b, nullptr, nullptr, 1, eps, y, yd, s);
 }
 

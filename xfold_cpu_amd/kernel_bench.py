@@ -1,0 +1,115 @@
+"""Per-kernel rates of the hot operators on one GPU, against MI355X peaks (HBM 8 TB/s, bf16
+dense MFMA 2.5 PFLOP/s).
+
+    python -m xfold_cpu_amd.kernel_bench [--n 768] [--reps 20]
+
+Each operator runs on synthetic bf16 inputs of the Pairformer shapes (pair [N, N, 128]) with
+the library's own HIP-event timing (``xfh_set_kernel_timing``) on, so every figure is the
+average duration of that kernel's launches on its stream. Bytes are the algorithmic HBM bytes
+of one launch (each input read once, each output written once); FLOPs count multiply-adds
+as two. One JSON line per kernel.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+
+import torch
+
+from . import nn as hnn
+from .fastnn import native_hip as nh
+from .fastnn import ops
+from .synthetic import init_module_
+
+HBM_PEAK_GBS = 8000.0
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def _timed(names, fn, reps):
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    for name in names:
+        nh.kernel_timing_read(name)
+    nh.set_kernel_timing(True)
+    try:
+        for _ in range(reps):
+            fn()
+        torch.cuda.synchronize()
+    finally:
+        nh.set_kernel_timing(False)
+    out = {}
+    for name in names:
+        total_ms, launches = nh.kernel_timing_read(name)
+        out[name] = (total_ms / launches if launches else float("nan"), launches)
+    return out
+
+
+def _line(kernel, workload, ms, launches, gbytes=None, gflop=None):
+    rec = {"kernel": kernel, "workload": workload, "avg_us": round(ms * 1e3, 2), "launches": launches}
+    if gbytes is not None:
+        rate = gbytes / ms                        # GB per ms = TB/s
+        rec.update(bytes_per_launch=gbytes * 1e9, hbm_tbs=round(rate, 3),
+                   hbm_frac=round(rate * 1e3 / HBM_PEAK_GBS, 3))
+    if gflop is not None:
+        tf = gflop / ms                           # GFLOP per ms = TFLOP/s
+        rec.update(flops_per_launch=gflop * 1e9, tflops=round(tf, 1), mfma_frac=round(tf / MFMA_PEAK_TFLOPS, 3))
+    print(json.dumps(rec), flush=True)
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    p.add_argument("--n", type=int, default=768)
+    p.add_argument("--reps", type=int, default=20)
+    args = p.parse_args(argv)
+    n, c = args.n, 128
+    dev = torch.device("cuda:0")
+    torch.manual_seed(0)
+    rows = n * n
+    pair = torch.randn(n, n, c, device=dev).bfloat16()
+    mask = torch.ones(n, n, device=dev)
+    gb_pair = rows * c * 2 / 1e9                  # one bf16 pass over the pair
+    with torch.inference_mode():
+        # LayerNorm over the pair rows, bf16 -> bf16 and fp32 -> bf16.
+        w, b = torch.ones(c, device=dev), torch.zeros(c, device=dev)
+        r = _timed(["layer_norm"], lambda: ops.layer_norm(pair, (c,), w, b, 1e-5, out_dtype=torch.bfloat16), args.reps)
+        _line("ln_rows_vec", f"LayerNorm [{rows}, {c}] bf16 -> bf16", *r["layer_norm"], gbytes=2 * gb_pair)
+        pair32 = pair.float()
+        r = _timed(["layer_norm"], lambda: ops.layer_norm(pair32, (c,), w, b, 1e-5, out_dtype=torch.bfloat16), args.reps)
+        _line("ln_rows_vec", f"LayerNorm [{rows}, {c}] fp32 -> bf16", *r["layer_norm"], gbytes=3 * gb_pair)
+        del pair32
+        with torch.amp.autocast("cuda", dtype=torch.bfloat16):
+            # Pair transition (GLU 128 -> 2 x 512 -> 128), added into the pair in place.
+            tr = init_module_(hnn.Transition(c_x=c, num_intermediate_factor=4), seed=1).to(dev).eval()
+            r = _timed(["transition"], lambda: hnn.transition_hip(tr, pair, accumulate_into=pair), args.reps)
+            _line("transition_kernel", f"pair transition N={n}", *r["transition"], gbytes=2 * gb_pair,
+                  gflop=2 * rows * (c * 1024 + 512 * c) / 1e9)
+            # Triangle multiplication (outgoing): projection, contraction, output.
+            tm = init_module_(hnn.TriangleMultiplication(c_pair=c, _outgoing=True), seed=2).to(dev).eval()
+            names = ["trimul_project", "trimul_contract", "trimul_output"]
+            r = _timed(names, lambda: hnn.triangle_multiplication_hip(tm, pair, mask, accumulate_into=pair),
+                       args.reps)
+            _line("trimul_project_kernel", f"TriMul projection N={n}", *r["trimul_project"], gbytes=3 * gb_pair)
+            _line("contraction_kernel", f"TriMul contraction N={n}", *r["trimul_contract"], gbytes=3 * gb_pair,
+                  gflop=2 * c * n ** 3 / 1e9)
+            _line("trimul_output_kernel", f"TriMul output N={n}", *r["trimul_output"], gbytes=3 * gb_pair)
+            # Triangle attention (starting node): projection, attention core, output.
+            ga = init_module_(hnn.GridSelfAttention(c_pair=c, num_head=4, transpose=False), seed=3).to(dev).eval()
+            npad = (n + 63) // 64 * 64
+            names = ["grid_project", "grid_attention", "grid_output"]
+            r = _timed(names, lambda: hnn.grid_self_attention_hip(ga, pair, mask, accumulate_into=pair), args.reps)
+            proj_gb = gb_pair + (rows * c + 2 * n * 4 * npad * 32) * 2 / 1e9 + 4 * n * npad * 4 / 1e9
+            _line("grid_project_kernel", f"TriAtt projection N={n}", *r["grid_project"], gbytes=proj_gb)
+            _line("grid_attention_kernel", f"TriAtt core N={n}, 4 heads x 32", *r["grid_attention"],
+                  gflop=4 * n * 4 * n * n * 32 / 1e9)
+            _line("grid_output_kernel", f"TriAtt output N={n}", *r["grid_output"], gbytes=3 * gb_pair)
+            # Pair-logits attention bias (single-track attention, 16 heads).
+            wl = (torch.randn(16, c, device=dev) / c ** 0.5).bfloat16()
+            r = _timed(["pair_bias"], lambda: ops.pair_attention_bias(pair, w, b, 1e-5, wl), args.reps)
+            _line("pair_bias_kernel", f"pair logits N={n}, 16 heads", *r["pair_bias"],
+                  gbytes=gb_pair + 16 * n * npad * 4 / 1e9)
+
+
+if __name__ == "__main__":
+    main()
