@@ -2,7 +2,7 @@
 // (grid_attention.hip): one preparation launch turns the caller's strided q, k, v, bias and
 // mask into that kernel's layouts, then the kernel runs at head dim 32 or 64.
 //
-// Preparation (one launch per part):
+// Preparation (one launch; each part takes its own range of workgroups):
 //   0  q  [B][H][Nq][D]   = q * scale * log2(e), zero for d >= Dqk
 //   1  k  [B][H][Npad][D] = k, zero for keys >= N or d >= Dqk
 //   2  vt [B][H][D][Npad] = v^T, zero for keys >= N or d >= Dv; inside each run of 32 keys
@@ -28,15 +28,22 @@ struct MhaPrep {
   float *bias;
   uint64_t *words;
   bool vec_qk;               // q and k rows hold whole 16-byte chunks (D, strides % 8, aligned)
+  // One launch runs every part: blocks [start[j], start[j + 1]) run part id[j].
+  int nparts;
+  int id[5];
+  int64_t start[6];
 };
 
 template <typename T> __device__ __forceinline__ float ld(const void *p, int64_t i) {
   return static_cast<float>(static_cast<const T *>(p)[i]);
 }
 
-__global__ void mha_prepare_kernel(MhaPrep p, int part) {
+__global__ void mha_prepare_kernel(MhaPrep p) {
   const AttentionArgs &a = p.a;
-  const int64_t idx = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int j = 0;
+  while (j + 1 < p.nparts && int64_t(blockIdx.x) >= p.start[j + 1]) ++j;
+  const int part = p.id[j];
+  const int64_t idx = (int64_t(blockIdx.x) - p.start[j]) * blockDim.x + threadIdx.x;
   const int D = p.D, dc = D / 8;            // 8-element chunks per row
   switch (part) {
     case 0: {                               // q: thread = (b, h, n, chunk)
@@ -215,14 +222,19 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
                           a.bs[2] % 8 == 0 && a.bs[3] % 8 == 0 &&
                           reinterpret_cast<uintptr_t>(a.bias) % 16 == 0;
   const bool packed = a.bias && a.bias_dtype == XFH_BIAS_PACKED;
+  p.nparts = 0;
+  p.start[0] = 0;
   for (int part = 0; part < 5; ++part) {
     if (part == 3 && packed) continue;             // already in the kernel's layout
     const int64_t n_work = part == 3 && head_minor ? a.Q * pl.npad : work[part];
     const int64_t blocks = ceil_div(n_work, 256);
     if (blocks == 0) continue;
-    if (blocks > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "dot_product_attention: problem too large");
-    mha_prepare_kernel<<<dim3(unsigned(blocks)), 256, 0, s>>>(p, part == 3 && head_minor ? 5 : part);
+    p.id[p.nparts] = part == 3 && head_minor ? 5 : part;
+    p.start[p.nparts + 1] = p.start[p.nparts] + blocks;
+    ++p.nparts;
   }
+  if (p.start[p.nparts] > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "dot_product_attention: problem too large");
+  if (p.nparts > 0) mha_prepare_kernel<<<dim3(unsigned(p.start[p.nparts])), 256, 0, s>>>(p);
   XFH_TRY(check_launch("mha_prepare"));
 
   GridAttentionArgs ga;
