@@ -65,12 +65,13 @@ def test_golden_bf16_pairformer_block(device):
         assert_parity_bf16(got[key], exact, f"golden bf16 block/{key}", stores=stores)
 
 
-def block_case(n, c_single, mode, pad, seed, device, with_single=True):
+def block_case(n, c_single, mode, pad, seed, device, with_single=True, c_pair=128, factor=4):
     """mode: 'fp32' (fp32 pair, no autocast), 'bf16-compute' (fp32 pair, bf16 autocast),
     'bf16' (bf16 pair and single under bf16 autocast, the C2-C5 protocol)."""
-    args = dict(n_heads=16, c_pair=128, c_single=c_single, n_heads_pair=4, with_single=with_single)
+    args = dict(n_heads=16, c_pair=c_pair, c_single=c_single, n_heads_pair=4, with_single=with_single,
+                num_intermediate_factor=factor)
     ref, hip = pair_of("PairformerBlock", args, seed=seed, device=device)
-    inp = pair_block_inputs(n, c_single=c_single, pad=pad, seed=seed, with_single=with_single)
+    inp = pair_block_inputs(n, c_pair=c_pair, c_single=c_single, pad=pad, seed=seed, with_single=with_single)
     pair, single = inp.pair, inp.single
     if mode == "bf16":
         pair = pair.bfloat16()
@@ -109,6 +110,20 @@ def test_pairformer_block(device, n, mode):
         assert gp.dtype == torch.bfloat16
         assert_parity_bf16(gp, wp, "pair", stores=5)
         assert_parity_bf16(gs, ws, "single", stores=2)
+
+
+@pytest.mark.parametrize("n,mode", [(40, "fp32"), (40, "bf16"), (150, "bf16")])
+def test_template_pairformer_block(device, n, mode):
+    """The template stack's block (xfold/nn/template.py:192-195): c_pair 64, transition
+    factor 2, 4 pair heads of 16 channels, no single track."""
+    announce("template_block", n, mode)
+    (gp, wp), _ = block_case(n, 0, mode, pad=2, seed=n + 7, device=device, with_single=False,
+                             c_pair=64, factor=2)
+    if mode == "fp32":
+        assert_parity(gp, wp, TOL_FP32, "pair")
+    else:
+        assert gp.dtype == torch.bfloat16
+        assert_parity_bf16(gp, wp, "pair", stores=5)
 
 
 def test_pairformer_block_updates_in_place(device):

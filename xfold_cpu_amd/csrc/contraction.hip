@@ -48,7 +48,7 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wi = wave >> 1, wj = wave & 1, col = lane & 15, grp = lane >> 4;
-  const int64_t opsize = int64_t(n) * ld;
+  const int64_t opsize = a.op_plane;
   const bf16 *L = a.left + ch * opsize;
   const bf16 *R = a.right + ch * opsize;
 
@@ -108,7 +108,7 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
   }
 
   // acc[x][y][e] = out[i = i0 + wi*96 + y*16 + col][j = j0 + wj*96 + x*16 + grp*4 + e]
-  bf16 *O = a.out + ch * int64_t(n) * n;
+  bf16 *O = a.out + ch * a.out_plane;
   const bool vec = (n % 4) == 0;
 #pragma unroll
   for (int y = 0; y < NT; ++y) {
@@ -139,6 +139,8 @@ int64_t contraction_ld(int64_t n) { return align_up(n, TK); }
 int contraction(const ContractionArgs &a, hipStream_t s) {
   if (a.n == 0 || a.channels == 0) return XFH_OK;
   if (a.ld != contraction_ld(a.n)) return fail(XFH_EINVAL, "contraction: operand rows must be padded to 32");
+  if (a.op_plane < int64_t(a.n) * a.ld || a.out_plane < int64_t(a.n) * a.n || a.op_plane % 8 || a.out_plane % 8)
+    return fail(XFH_EINVAL, "contraction: channel planes overlap or are not 16-byte aligned");
   const int64_t tiles = ceil_div(a.n, TB);
   const int64_t total = tiles * tiles * a.channels;
   const int64_t grid = ceil_div(total, 8) * 8;

@@ -42,23 +42,18 @@ template <typename TIN>
 __global__ __launch_bounds__(512, 1) void grid_project_kernel(GridProjectArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 w_lds[W_ROWS * K];
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
-  for (int i = threadIdx.x; i < W_ROWS * 16; i += blockDim.x) {
-    const int r = i >> 4, c = i & 15;               // LDS row, 16-byte chunk
+  rowstep::WeightStage<W_ROWS, 512> sw;
+  rowstep::LnStage sl;
+  sw.load([&](int r) -> const bf16 * {
     const int blk = r / K, rr = r % K;              // q, k, v, bias
-    const bf16 *src = nullptr;
     if (blk < 2) {                                  // q, k: rows permuted inside each head
       const int t = rr / 16, e = rr % 16;
-      src = (blk == 0 ? a.wq : a.wk) + (32 * (t / 2) + 8 * (e / 4) + 4 * (t % 2) + (e % 4)) * K;
-    } else if (blk == 2) {
-      src = a.wv + rr * K;
-    } else if (rr < a.heads) {
-      src = a.wb + rr * K;
+      return (blk == 0 ? a.wq : a.wk) + (32 * (t / 2) + 8 * (e / 4) + 4 * (t % 2) + (e % 4)) * K;
     }
-    bf16x8 v = {};
-    if (src) v = *reinterpret_cast<const bf16x8 *>(src + c * 8);
-    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) = v;
-  }
-  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
+    if (blk == 2) return a.wv + rr * K;
+    return rr < a.heads ? a.wb + rr * K : nullptr;
+  }, false);
+  sl.load(a.ln_w, a.ln_b);
 
   const int n = a.n, H = a.heads, npad = a.npad, upr = npad / 32;
   const int units = n * upr;
@@ -75,7 +70,6 @@ __global__ __launch_bounds__(512, 1) void grid_project_kernel(GridProjectArgs a)
       if (lane == 0) a.maskbits[wd] = ballot;
     }
   }
-  __syncthreads();
   const TIN *z = static_cast<const TIN *>(a.pair);
   // Pair row of attention position (b, t): b*n + t (starting node) or t*n + b (ending node).
   auto pos_of = [&](int b, int t) -> int64_t { return a.transpose ? int64_t(t) * n + b : int64_t(b) * n + t; };
@@ -92,7 +86,10 @@ __global__ __launch_bounds__(512, 1) void grid_project_kernel(GridProjectArgs a)
   };
   int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
   Unit cur;
-  if (u < units) fetch(u, cur);
+  if (u < units) fetch(u, cur);                     // in flight while the weights are stored
+  sw.store(w_lds);
+  sl.store(lnw, lnb);
+  __syncthreads();
   for (; u < units; u += waves) {
     Unit next;
     if (u + waves < units) fetch(u + waves, next);
@@ -220,10 +217,11 @@ __global__ __launch_bounds__(512, 1) void grid_output_kernel(GridOutputArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 w_gate[rowstep::W_ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 w_out[rowstep::W_ELEMS];
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
-  rowstep::load_weight(a.w_gating, w_gate, false);
-  rowstep::load_weight(a.w_out, w_out, true);
-  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
-  __syncthreads();
+  rowstep::WeightStage<K, 512> sg, so;
+  rowstep::LnStage sl;
+  sg.load([&](int row) { return a.w_gating + row * K; }, false);
+  so.load([&](int row) { return a.w_out + row * K; }, true);
+  sl.load(a.ln_w, a.ln_b);
 
   const int64_t npos = int64_t(a.n) * a.n;
   const int64_t steps = (npos + 15) / 16;
@@ -253,7 +251,11 @@ __global__ __launch_bounds__(512, 1) void grid_output_kernel(GridOutputArgs a) {
   // Rows of the next step are loaded while this one is computed.
   int64_t st = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   Rows cur;
-  if (st < steps) fetch(st, cur);
+  if (st < steps) fetch(st, cur);                   // in flight while the weights are stored
+  sg.store(w_gate);
+  so.store(w_out);
+  sl.store(lnw, lnb);
+  __syncthreads();
   for (; st < steps; st += waves) {
     Rows next;
     if (st + waves < steps) fetch(st + waves, next);

@@ -124,11 +124,13 @@ struct TriProjectArgs {
   float eps;
   const bf16 *w_proj, *w_gate;  // [2c][c] each (nn.Linear layout)
   bf16 *left, *right;        // [c][n][ld] contraction operands (contraction_ld), zero-padded
+  int64_t plane;             // elements from one channel's operand plane to the next (>= n ld)
   int n, ld, outgoing;
 };
 struct TriOutputArgs {
   const void *pair;
-  const bf16 *contracted;    // [c][n][n]
+  const bf16 *contracted;    // [c][n][n], planes c_plane elements apart
+  int64_t c_plane;
   const float *ln_in_w, *ln_in_b;
   float eps_in;
   const float *ln_c_w, *ln_c_b;
@@ -153,6 +155,7 @@ int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStr
 struct ContractionArgs {
   const bf16 *left, *right;  // [channels][n][ld], k-contiguous rows, zero for k >= n
   bf16 *out;                 // [channels][n][n]
+  int64_t op_plane, out_plane;  // elements between channel planes (>= n ld, >= n n)
   int n, ld, channels;
 };
 int64_t contraction_ld(int64_t n);

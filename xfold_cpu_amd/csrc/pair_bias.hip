@@ -30,14 +30,10 @@ __global__ __launch_bounds__(512, 1) void pair_bias_kernel(PairBiasArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 w_lds[MAX_HEADS * K];
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
   const int tiles = (a.heads + 15) / 16;
-  for (int i = threadIdx.x; i < tiles * 16 * 16; i += blockDim.x) {
-    const int r = i >> 4, c = i & 15;               // LDS row, 16-byte chunk
-    bf16x8 v = {};
-    if (r < a.heads) v = *reinterpret_cast<const bf16x8 *>(a.w + int64_t(r) * K + c * 8);
-    *reinterpret_cast<bf16x8 *>(w_lds + r * K + ((c ^ (r & 15)) * 8)) = v;
-  }
-  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
-  __syncthreads();
+  rowstep::WeightStage<MAX_HEADS, 512> sw;          // rows >= heads are zeros
+  rowstep::LnStage sl;
+  sw.load([&](int r) { return r < a.heads ? a.w + int64_t(r) * K : nullptr; }, false);
+  sl.load(a.ln_w, a.ln_b);
 
   const int n = a.n, npad = a.npad, upr = npad / 32;
   const int units = n * upr;
@@ -57,7 +53,10 @@ __global__ __launch_bounds__(512, 1) void pair_bias_kernel(PairBiasArgs a) {
   };
   int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
   Unit cur;
-  if (u < units) fetch(u, cur);
+  if (u < units) fetch(u, cur);                     // in flight while the weights are stored
+  sw.store(w_lds);
+  sl.store(lnw, lnb);
+  __syncthreads();
   for (; u < units; u += waves) {
     Unit next;
     if (u + waves < units) fetch(u + waves, next);

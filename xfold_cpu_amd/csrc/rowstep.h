@@ -31,27 +31,48 @@ __host__ __device__ constexpr int kperm(int ks, int g, int j) {
   return j < 4 ? 32 * ks + 4 * g + j : 32 * ks + 16 + 4 * g + (j - 4);
 }
 
-// Copies W ([rows][128] bf16, row-major) into LDS with the chunk swizzle; `permuted`
-// reorders each row's input channels to kperm order. All threads of the workgroup take part.
-__device__ __forceinline__ void load_weight(const bf16 *__restrict__ w, bf16 *dst, bool permuted, int rows = C) {
-  for (int i = threadIdx.x; i < rows * 16; i += blockDim.x) {
-    const int n = i >> 4, c = i & 15;              // destination row, logical chunk
-    const int ks = c >> 2, g = c & 3;
-    bf16x8 v;
-    if (permuted) {
-      const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(w + n * C + kperm(ks, g, 0));
-      const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(w + n * C + kperm(ks, g, 4));
+// Weight rows ([rows][128] bf16, row-major) on their way into LDS with the chunk swizzle:
+// load() issues every global load of the calling thread, store() writes them, so the copy
+// costs one memory round trip (a loop that stores each chunk before loading the next pays
+// one per iteration). Work is spread over T threads (the workgroup size); `src(row)` gives
+// the row's source, or nullptr for a row of zeros; `permuted` reorders each row's input
+// channels to kperm order.
+template <int ROWS, int T> struct WeightStage {
+  static constexpr int N = (ROWS * 16 + T - 1) / T;   // chunks per thread
+  bf16x8 v[N];
+  template <class Src> __device__ __forceinline__ void load(Src src, bool permuted) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = lo[e];
-        v[4 + e] = hi[e];
+    for (int j = 0; j < N; ++j) {
+      const int i = int(threadIdx.x) + j * T;
+      v[j] = bf16x8{};
+      if (i >= ROWS * 16) continue;
+      const int n = i >> 4, c = i & 15;             // row, logical chunk
+      const bf16 *w = src(n);
+      if (!w) continue;
+      if (permuted) {
+        const int ks = c >> 2, g = c & 3;
+        const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(w + kperm(ks, g, 0));
+        const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(w + kperm(ks, g, 4));
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[j][e] = lo[e];
+          v[j][4 + e] = hi[e];
+        }
+      } else {
+        v[j] = *reinterpret_cast<const bf16x8 *>(w + c * 8);
       }
-    } else {
-      v = *reinterpret_cast<const bf16x8 *>(w + n * C + c * 8);
     }
-    *reinterpret_cast<bf16x8 *>(dst + n * C + ((c ^ (n & 15)) * 8)) = v;
   }
-}
+  __device__ __forceinline__ void store(bf16 *dst) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int i = int(threadIdx.x) + j * T;
+      if (i >= ROWS * 16) continue;
+      const int n = i >> 4, c = i & 15;
+      *reinterpret_cast<bf16x8 *>(dst + n * C + ((c ^ (n & 15)) * 8)) = v[j];
+    }
+  }
+};
 
 // Fragment of W for output tile t, k-step ks (lane: row 16 t + l % 16, chunk 4 ks + g):
 // the A operand of out^T = W . x^T, or the B operand of out = x . W^T (same lane layout).
@@ -196,6 +217,27 @@ __device__ __forceinline__ void ln_k(float (&v)[32], const float *lnw, const flo
     for (int j = 0; j < 8; ++j) x[ks][j] = bf16((v[8 * ks + j] - mean) * rstd * wv[j] + bv[j]);
   }
 }
+
+// Optional LayerNorm affine parameters (fp32[128], nullptr: 1 / 0) on their way into LDS,
+// split like WeightStage; the workgroup has at least 128 threads.
+struct LnStage {
+  float w, b;
+  __device__ __forceinline__ void load(const float *wp, const float *bp) {
+    const int i = int(threadIdx.x);
+    w = 1.f;
+    b = 0.f;
+    if (i < C) {
+      if (wp) w = wp[i];
+      if (bp) b = bp[i];
+    }
+  }
+  __device__ __forceinline__ void store(float *w_lds, float *b_lds) const {
+    if (threadIdx.x < C) {
+      w_lds[threadIdx.x] = w;
+      b_lds[threadIdx.x] = b;
+    }
+  }
+};
 
 // Copies optional LayerNorm affine parameters (fp32[128], nullptr: 1 / 0) into LDS.
 __device__ __forceinline__ void load_ln(const float *w, const float *b, float *w_lds, float *b_lds) {

@@ -149,9 +149,11 @@ __global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(Trans
       dma16(seg < 16 ? w1c : w2c, src_off[j], slot + seg * 512);
     }
   };
-  load_ln(a.ln_w, a.ln_b, lnw, lnb);
+  LnStage sl;
+  sl.load(a.ln_w, a.ln_b);
   if (total_chunks > 0) issue(0);
   if (total_chunks > 1) issue(1);
+  sl.store(lnw, lnb);                                // (its loads are older than the chunks')
   __syncthreads();                                   // LayerNorm parameters
 
   int gc = 0;                                        // chunks consumed so far

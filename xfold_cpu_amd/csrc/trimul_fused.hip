@@ -46,17 +46,18 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
   __shared__ __attribute__((aligned(16))) bf16 w_proj[PROJ * K];
   __shared__ __attribute__((aligned(16))) bf16 w_gate[PROJ * K];
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
-  rowstep::load_weight(a.w_proj, w_proj, false, PROJ);
-  rowstep::load_weight(a.w_gate, w_gate, false, PROJ);
-  rowstep::load_ln(a.ln_w, a.ln_b, lnw, lnb);
-  __syncthreads();
+  rowstep::WeightStage<PROJ, 512> sp, sg;
+  rowstep::LnStage sl;
+  sp.load([&](int row) { return a.w_proj + row * K; }, false);
+  sg.load([&](int row) { return a.w_gate + row * K; }, false);
+  sl.load(a.ln_w, a.ln_b);
 
   const int n = a.n, cpr = a.ld / UP;               // units per grid line
   const int units = n * cpr;                        // < 2^31 (n * ld fits in 32 bits)
   const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
   const int waves = int(gridDim.x) * int(blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
-  const int64_t plane = int64_t(n) * a.ld;
+  const int64_t plane = a.plane;
   // Pair position of grid-line entry (x, y): (x, y) outgoing, (y, x) incoming.
   auto pos_of = [&](int x, int y) -> int64_t { return a.outgoing ? int64_t(x) * n + y : int64_t(y) * n + x; };
 
@@ -76,7 +77,11 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
   };
   int u = int(blockIdx.x) * int(blockDim.x >> 6) + int(threadIdx.x >> 6);
   Unit cur;
-  if (u < units) fetch(u, cur);
+  if (u < units) fetch(u, cur);                     // in flight while the weights are stored
+  sp.store(w_proj);
+  sg.store(w_gate);
+  sl.store(lnw, lnb);
+  __syncthreads();
   for (; u < units; u += waves) {
     Unit next;
     if (u + waves < units) fetch(u + waves, next);
@@ -145,11 +150,12 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
   __shared__ __attribute__((aligned(16))) bf16 w_gate[rowstep::W_ELEMS];
   __shared__ __attribute__((aligned(16))) bf16 w_out[rowstep::W_ELEMS];
   __shared__ __attribute__((aligned(16))) float lnw_in[K], lnb_in[K], lnw_c[K], lnb_c[K];
-  rowstep::load_weight(a.w_gating, w_gate, false);
-  rowstep::load_weight(a.w_out, w_out, true);
-  rowstep::load_ln(a.ln_in_w, a.ln_in_b, lnw_in, lnb_in);
-  rowstep::load_ln(a.ln_c_w, a.ln_c_b, lnw_c, lnb_c);
-  __syncthreads();
+  rowstep::WeightStage<K, 512> sg, so;
+  rowstep::LnStage sl_in, sl_c;
+  sg.load([&](int row) { return a.w_gating + row * K; }, false);
+  so.load([&](int row) { return a.w_out + row * K; }, true);
+  sl_in.load(a.ln_in_w, a.ln_in_b);
+  sl_c.load(a.ln_c_w, a.ln_c_b);
 
   const int64_t npos = int64_t(a.n) * a.n;
   const int64_t steps = (npos + 15) / 16;
@@ -160,7 +166,6 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
   constexpr bool kBf16 = sizeof(TIN) == 2 && sizeof(TOUT) == 2;
   const bool res_from_z = kBf16 && a.accumulate && a.pair == a.out;
   const bool res_load = a.accumulate && !res_from_z;
-  const bool c_vec = (npos % 8) == 0;
   bf16x8 id[2];
   rowstep::identity_frags(id);
 
@@ -177,9 +182,9 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
     const int64_t p0 = st * 16 + 8 * (g & 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bf16 *src = a.contracted + int64_t(16 * (q + 4 * (g >> 1)) + r) * npos + p0;
+      const bf16 *src = a.contracted + int64_t(16 * (q + 4 * (g >> 1)) + r) * a.c_plane + p0;
       bf16x8 v = {};
-      if (c_vec && p0 + 8 <= npos) {
+      if (p0 + 8 <= npos) {                      // planes start 16-byte aligned
         v = *reinterpret_cast<const bf16x8 *>(src);
       } else {
 #pragma unroll
@@ -193,7 +198,12 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
 
   int64_t st = int64_t(blockIdx.x) * (blockDim.x >> 6) + (threadIdx.x >> 6);
   Rows cur;
-  if (st < steps) fetch(st, cur);
+  if (st < steps) fetch(st, cur);                   // in flight while the weights are stored
+  sg.store(w_gate);
+  so.store(w_out);
+  sl_in.store(lnw_in, lnb_in);
+  sl_c.store(lnw_c, lnb_c);
+  __syncthreads();
   for (; st < steps; st += waves) {
     Rows next;
     if (st + waves < steps) fetch(st + waves, next);
@@ -281,6 +291,8 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
 
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
   if (a.ld % 32 != 0 || a.ld < a.n) return fail(XFH_EINVAL, "trimul_project: ld must be a multiple of 32, >= n");
+  if (a.plane < int64_t(a.n) * a.ld || a.plane % 8)
+    return fail(XFH_EINVAL, "trimul_project: operand planes overlap or are not 16-byte aligned");
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   // 32-position units unless that leaves fewer than four per wavefront (the last round of
@@ -302,6 +314,8 @@ int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
 
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s) {
   const int64_t steps = ceil_div(int64_t(a.n) * a.n, 16);
+  if (a.c_plane < int64_t(a.n) * a.n || a.c_plane % 8)
+    return fail(XFH_EINVAL, "trimul_output: result planes overlap or are not 16-byte aligned");
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(steps, 8))));
