@@ -43,6 +43,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--graph", action="store_true",
+                   help="capture one step in a HIP graph after the warm-up and time its replays")
     p.add_argument("--copy-calibration-mb", type=int, default=0,
                    help="after the run, read and write a buffer of this many MiB once (a plain copy "
                         "kernel of known size whose FETCH_SIZE/WRITE_SIZE counters calibrate the "
@@ -206,12 +208,21 @@ def main():
         if i == 0 or i + 1 == args.warmup:
             log(f"warmup {i + 1}/{args.warmup}")
     torch.cuda.synchronize()
+    run = step
+    if args.graph:
+        # The step records no memset, host copy or synchronisation, so it replays as a graph.
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        torch.cuda.synchronize()
+        run = graph.replay
+        log("captured one step in a HIP graph")
     stream = torch.cuda.current_stream(device)
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
     for _ in range(args.steps):
-        step()
+        run()
     stop.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
@@ -244,7 +255,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,1/fan_in) weights)",
-        "config": workload, "roofline": roof, "cpu_baseline": base,
+        "config": dict(workload, launch="hip graph replay" if args.graph else "eager"),
+        "roofline": roof, "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)
 
