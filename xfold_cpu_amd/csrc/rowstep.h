@@ -239,14 +239,6 @@ struct LnStage {
   }
 };
 
-// Copies optional LayerNorm affine parameters (fp32[128], nullptr: 1 / 0) into LDS.
-__device__ __forceinline__ void load_ln(const float *w, const float *b, float *w_lds, float *b_lds) {
-  for (int i = threadIdx.x; i < C; i += blockDim.x) {
-    w_lds[i] = w ? w[i] : 1.f;
-    b_lds[i] = b ? b[i] : 0.f;
-  }
-}
-
 // Identity fragments: as the A operand with a K-layout operand x[ks] as B, half h
 // (0 or 1) gives O-layout tile t = 2 ks + h exactly (one nonzero product per output), so
 // one MFMA both converts 16 bf16 channels per position to fp32 and moves them into O-layout.
