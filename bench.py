@@ -124,15 +124,22 @@ def build_workload(cfg_name, device):
 ATTENTION_TRAFFIC_BYTES = {384: 168.25e6, 768: 1037.9e6}
 
 
+PAIR_TIMERS = ("transition", "trimul_project", "trimul_contract", "trimul_output", "grid_project",
+               "grid_attention", "grid_output", "pair_bias")
+
+
 def kernel_roofline(step, n, steps):
-    """Average duration of the dominant kernel (triangle attention core: B=N rows, 4 heads
-    x 32, N x N keys, pair bias and 2-D key mask) inside the block workload, from HIP events
-    the library records around each launch on the launch stream."""
+    """Average launch duration of every pair-stack kernel inside the block workload, from HIP
+    events the library records around each launch on the launch stream, with its HBM or MFMA
+    rate (algorithmic bytes / FLOPs of one launch, xfold_cpu_amd.kernel_bench). Returns the
+    roofline object of the dominant kernel (triangle attention core: B=N rows, 4 heads x 32,
+    N x N keys, pair bias and 2-D key mask) and the per-kernel table."""
     import torch
     from xfold_cpu_amd.fastnn import native_hip
+    from xfold_cpu_amd.kernel_bench import pair_kernel_work, rates
 
-    name = "grid_attention"
-    native_hip.kernel_timing_read(name)               # drop anything recorded earlier
+    for name in PAIR_TIMERS:
+        native_hip.kernel_timing_read(name)           # drop anything recorded earlier
     native_hip.set_kernel_timing(True)
     try:
         for _ in range(steps):
@@ -140,9 +147,18 @@ def kernel_roofline(step, n, steps):
         torch.cuda.synchronize()
     finally:
         native_hip.set_kernel_timing(False)
-    total_ms, launches = native_hip.kernel_timing_read(name)
+    timed = {name: native_hip.kernel_timing_read(name) for name in PAIR_TIMERS}
+    work = pair_kernel_work(n)
+    kernels = {}
+    for name, (total_ms, launches) in timed.items():
+        if launches:
+            kernel, gbytes, gflop = work[name]
+            r = rates(total_ms / launches, gbytes, gflop)
+            kernels[kernel] = dict(avg_us=round(total_ms / launches * 1e3, 2), launches=launches,
+                                   **{k: r[k] for k in ("hbm_tbs", "hbm_frac", "tflops", "mfma_frac") if k in r})
+    total_ms, launches = timed["grid_attention"]
     if launches == 0:
-        return None
+        return None, kernels
     ms = total_ms / launches
     heads, d = 4, 32
     flops = 4.0 * n * heads * n * n * d            # Q.K^T and P.V over all N^3 logits
@@ -151,7 +167,7 @@ def kernel_roofline(step, n, steps):
             "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": ATTENTION_TRAFFIC_BYTES.get(n),
             "avg_launch_ms": round(ms, 4), "launches": launches, "flops_per_launch": flops,
-            "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}
+            "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}, kernels
 
 
 def cpu_baseline(cfg, budget_s=30.0):
@@ -230,9 +246,9 @@ def main():
     log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
     value = ms_step / blocks
 
-    roof = None
+    roof, kernels = None, None
     if cfg["kind"] != "diffusion":
-        roof = kernel_roofline(step, cfg["n"], max(1, min(args.steps, 5)))
+        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(args.steps, 5)))
         log(f"roofline: {roof}")
     base = None
     if not args.no_cpu_baseline:
@@ -256,7 +272,7 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,1/fan_in) weights)",
         "config": dict(workload, launch="hip graph replay" if args.graph else "eager"),
-        "roofline": roof, "cpu_baseline": base,
+        "roofline": roof, "cpu_baseline": base, "kernels": kernels,
     }
     print(json.dumps(line), flush=True)
 

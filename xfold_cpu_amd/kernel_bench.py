@@ -26,6 +26,40 @@ HBM_PEAK_GBS = 8000.0
 MFMA_PEAK_TFLOPS = 2500.0
 
 
+def pair_kernel_work(n: int, c: int = 128, heads: int = 4, head_dim: int = 32, bias_heads: int = 16):
+    """Algorithmic work of one launch of each pair-stack kernel at N tokens: {timer name:
+    (kernel, GB or None, GFLOP or None)}. Bytes count each input read once and each output
+    written once (bf16 pair, fp32 attention bias); FLOPs count multiply-adds as two."""
+    rows = n * n
+    npad = (n + 63) // 64 * 64
+    gb_pair = rows * c * 2 / 1e9                  # one bf16 pass over the pair
+    return {
+        "transition": ("transition_kernel", 2 * gb_pair, 2 * rows * (c * 8 * c + 4 * c * c) / 1e9),
+        "trimul_project": ("trimul_project_kernel", 3 * gb_pair, None),
+        "trimul_contract": ("contraction_kernel", 3 * gb_pair, 2 * c * n ** 3 / 1e9),
+        "trimul_output": ("trimul_output_kernel", 3 * gb_pair, None),
+        "grid_project": ("grid_project_kernel",
+                         gb_pair + (rows * c + 2 * n * heads * npad * head_dim) * 2 / 1e9 + heads * n * npad * 4 / 1e9,
+                         None),
+        "grid_attention": ("grid_attention_kernel", None, 4 * n * heads * n * n * head_dim / 1e9),
+        "grid_output": ("grid_output_kernel", 3 * gb_pair, None),
+        "pair_bias": ("pair_bias_kernel", gb_pair + bias_heads * n * npad * 4 / 1e9, None),
+    }
+
+
+def rates(ms, gbytes=None, gflop=None):
+    """HBM and MFMA rates of one launch of `ms` milliseconds against the MI355X peaks."""
+    rec = {}
+    if gbytes is not None:
+        rate = gbytes / ms                        # GB per ms = TB/s
+        rec.update(bytes_per_launch=gbytes * 1e9, hbm_tbs=round(rate, 3),
+                   hbm_frac=round(rate * 1e3 / HBM_PEAK_GBS, 3))
+    if gflop is not None:
+        tf = gflop / ms                           # GFLOP per ms = TFLOP/s
+        rec.update(flops_per_launch=gflop * 1e9, tflops=round(tf, 1), mfma_frac=round(tf / MFMA_PEAK_TFLOPS, 3))
+    return rec
+
+
 def _timed(names, fn, reps):
     for _ in range(3):
         fn()
@@ -48,13 +82,7 @@ def _timed(names, fn, reps):
 
 def _line(kernel, workload, ms, launches, gbytes=None, gflop=None):
     rec = {"kernel": kernel, "workload": workload, "avg_us": round(ms * 1e3, 2), "launches": launches}
-    if gbytes is not None:
-        rate = gbytes / ms                        # GB per ms = TB/s
-        rec.update(bytes_per_launch=gbytes * 1e9, hbm_tbs=round(rate, 3),
-                   hbm_frac=round(rate * 1e3 / HBM_PEAK_GBS, 3))
-    if gflop is not None:
-        tf = gflop / ms                           # GFLOP per ms = TFLOP/s
-        rec.update(flops_per_launch=gflop * 1e9, tflops=round(tf, 1), mfma_frac=round(tf / MFMA_PEAK_TFLOPS, 3))
+    rec.update(rates(ms, gbytes, gflop))
     print(json.dumps(rec), flush=True)
 
 
@@ -70,6 +98,7 @@ def main(argv=None):
     pair = torch.randn(n, n, c, device=dev).bfloat16()
     mask = torch.ones(n, n, device=dev)
     gb_pair = rows * c * 2 / 1e9                  # one bf16 pass over the pair
+    work = pair_kernel_work(n, c)
     with torch.inference_mode():
         # LayerNorm over the pair rows, bf16 -> bf16 and fp32 -> bf16.
         w, b = torch.ones(c, device=dev), torch.zeros(c, device=dev)
@@ -83,32 +112,27 @@ def main(argv=None):
             # Pair transition (GLU 128 -> 2 x 512 -> 128), added into the pair in place.
             tr = init_module_(hnn.Transition(c_x=c, num_intermediate_factor=4), seed=1).to(dev).eval()
             r = _timed(["transition"], lambda: hnn.transition_hip(tr, pair, accumulate_into=pair), args.reps)
-            _line("transition_kernel", f"pair transition N={n}", *r["transition"], gbytes=2 * gb_pair,
-                  gflop=2 * rows * (c * 1024 + 512 * c) / 1e9)
+            _line("transition_kernel", f"pair transition N={n}", *r["transition"], *work["transition"][1:])
             # Triangle multiplication (outgoing): projection, contraction, output.
             tm = init_module_(hnn.TriangleMultiplication(c_pair=c, _outgoing=True), seed=2).to(dev).eval()
             names = ["trimul_project", "trimul_contract", "trimul_output"]
             r = _timed(names, lambda: hnn.triangle_multiplication_hip(tm, pair, mask, accumulate_into=pair),
                        args.reps)
-            _line("trimul_project_kernel", f"TriMul projection N={n}", *r["trimul_project"], gbytes=3 * gb_pair)
-            _line("contraction_kernel", f"TriMul contraction N={n}", *r["trimul_contract"], gbytes=3 * gb_pair,
-                  gflop=2 * c * n ** 3 / 1e9)
-            _line("trimul_output_kernel", f"TriMul output N={n}", *r["trimul_output"], gbytes=3 * gb_pair)
+            _line("trimul_project_kernel", f"TriMul projection N={n}", *r["trimul_project"], *work["trimul_project"][1:])
+            _line("contraction_kernel", f"TriMul contraction N={n}", *r["trimul_contract"], *work["trimul_contract"][1:])
+            _line("trimul_output_kernel", f"TriMul output N={n}", *r["trimul_output"], *work["trimul_output"][1:])
             # Triangle attention (starting node): projection, attention core, output.
             ga = init_module_(hnn.GridSelfAttention(c_pair=c, num_head=4, transpose=False), seed=3).to(dev).eval()
-            npad = (n + 63) // 64 * 64
             names = ["grid_project", "grid_attention", "grid_output"]
             r = _timed(names, lambda: hnn.grid_self_attention_hip(ga, pair, mask, accumulate_into=pair), args.reps)
-            proj_gb = gb_pair + (rows * c + 2 * n * 4 * npad * 32) * 2 / 1e9 + 4 * n * npad * 4 / 1e9
-            _line("grid_project_kernel", f"TriAtt projection N={n}", *r["grid_project"], gbytes=proj_gb)
+            _line("grid_project_kernel", f"TriAtt projection N={n}", *r["grid_project"], *work["grid_project"][1:])
             _line("grid_attention_kernel", f"TriAtt core N={n}, 4 heads x 32", *r["grid_attention"],
-                  gflop=4 * n * 4 * n * n * 32 / 1e9)
-            _line("grid_output_kernel", f"TriAtt output N={n}", *r["grid_output"], gbytes=3 * gb_pair)
+                  *work["grid_attention"][1:])
+            _line("grid_output_kernel", f"TriAtt output N={n}", *r["grid_output"], *work["grid_output"][1:])
             # Pair-logits attention bias (single-track attention, 16 heads).
             wl = (torch.randn(16, c, device=dev) / c ** 0.5).bfloat16()
             r = _timed(["pair_bias"], lambda: ops.pair_attention_bias(pair, w, b, 1e-5, wl), args.reps)
-            _line("pair_bias_kernel", f"pair logits N={n}, 16 heads", *r["pair_bias"],
-                  gbytes=gb_pair + 16 * n * npad * 4 / 1e9)
+            _line("pair_bias_kernel", f"pair logits N={n}, 16 heads", *r["pair_bias"], *work["pair_bias"][1:])
 
 
 if __name__ == "__main__":
