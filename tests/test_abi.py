@@ -140,6 +140,32 @@ def test_weight_cache_reuses_and_invalidates():
     assert cache._key is None
 
 
+def test_derived_weight_rebuilds_when_a_source_changes():
+    """Weights derived from several parameters (stacked projections, folded LayerNorm
+    weights) are built once and rebuilt when any source is updated in place."""
+    module = torch.nn.Module()
+    a, b = torch.nn.Parameter(torch.randn(3, 4)), torch.nn.Parameter(torch.randn(2, 4))
+    calls = []
+
+    def build(*ws):
+        calls.append(1)
+        return torch.cat([w.detach() for w in ws], dim=0)
+
+    with torch.no_grad():
+        first = nh.derived_weight(module, "stack", [a, b], build)
+        assert nh.derived_weight(module, "stack", [a, b], build) is first and len(calls) == 1
+        b.mul_(2)
+        second = nh.derived_weight(module, "stack", [a, b], build)
+        assert second is not first and len(calls) == 2
+        torch.testing.assert_close(second, torch.cat([a, b]))
+        assert nh.derived_weight(module, "other", [a], build) is not second and len(calls) == 3
+    with torch.inference_mode():
+        c = torch.randn(2, 4)
+        nh.derived_weight(module, "inference", [c], build)
+        nh.derived_weight(module, "inference", [c], build)
+    assert len(calls) == 5                            # inference tensors are never cached
+
+
 @pytest.mark.parametrize("fixture,cls", [
     ("pairformer_block", "PairformerBlock"), ("diffusion_transformer", "DiffusionTransformer"),
     ("grid_attention_start", "GridSelfAttention"), ("self_attention_cond", "SelfAttention"),
