@@ -112,6 +112,22 @@ def test_pairformer_block(device, n, mode):
         assert_parity_bf16(gs, ws, "single", stores=2)
 
 
+@pytest.mark.parametrize("n,mode,pad", [(1, "fp32", 0), (1, "bf16", 0), (2, "bf16", 1), (3, "fp32", 0),
+                                        (3, "bf16", 3)])
+def test_pairformer_block_tiny(device, n, mode, pad):
+    """One to three tokens (one token padded, or all of them): every kernel's tail and
+    padding logic at its smallest, fully masked rows included."""
+    announce("pairformer_block tiny", n, mode, pad)
+    (gp, wp), (gs, ws) = block_case(n, 64, mode, pad=pad, seed=n + 3, device=device)
+    assert torch.isfinite(gp.float()).all() and torch.isfinite(gs.float()).all()
+    if mode == "fp32":
+        assert_parity(gp, wp, TOL_FP32, "pair")
+        assert_parity(gs, ws, TOL_FP32, "single")
+    else:
+        assert_parity_bf16(gp, wp, "pair", stores=5)
+        assert_parity_bf16(gs, ws, "single", stores=2)
+
+
 @pytest.mark.parametrize("n,mode", [(40, "fp32"), (40, "bf16"), (150, "bf16")])
 def test_template_pairformer_block(device, n, mode):
     """The template stack's block (xfold/nn/template.py:192-195): c_pair 64, transition

@@ -187,7 +187,8 @@ bool mha_supported(const AttentionArgs &a, int dtype) {
   return dtype == XFH_BF16 && a.out_dtype == XFH_BF16 && padded_dim(a.D > a.Dv ? a.D : a.Dv) != 0 &&
          a.K > 0 && align_up(a.K, 64) <= grid_attention_max_n() &&
          (!a.bias || a.bias_dtype == XFH_BIAS_PACKED || a.B == 1 || a.bs[0] == 0) &&  // batch-shared bias
-         (!a.mask || (a.ms[1] == 0 && a.ms[2] == 0)) &&      // mask per (batch entry, key)
+         // mask per (batch entry, key); a size-1 head or query dimension has no stride to speak of
+         (!a.mask || ((a.ms[1] == 0 || a.H == 1) && (a.ms[2] == 0 || a.Q == 1))) &&
          a.os[1] % 4 == 0 && a.os[2] % 4 == 0 && a.os[0] % 4 == 0 &&
          reinterpret_cast<uintptr_t>(a.o) % 8 == 0;
 }
