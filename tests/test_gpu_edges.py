@@ -1,0 +1,109 @@
+"""Edge sizes through the HIP modules and the attention entry point: one to three tokens,
+single queries and keys, every mask rank the reference accepts
+(xfold/fastnn/attention.py:57-62), against the oracle at the fp32 and bf16 bars."""
+
+import pytest
+import torch
+
+from oracle import restatement as R
+from tests.helpers import TOL_FP32, assert_parity, assert_parity_bf16
+from tests.test_gpu_ops import announce, autocast, pair_of, run_both
+from xfold_cpu_amd import fastnn
+
+pytestmark = pytest.mark.gpu
+
+
+def check(got, want, bf16, what):
+    assert torch.isfinite(got.float()).all(), what
+    if bf16:
+        assert_parity_bf16(got, want, what)
+    else:
+        assert_parity(got, want, TOL_FP32, what)
+
+
+def pair_case(n, seed, masked_last=False):
+    g = torch.Generator().manual_seed(seed)
+    pair = torch.randn(n, n, 128, generator=g)
+    seq = torch.ones(n)
+    if masked_last:
+        seq[-1] = 0
+    return pair, seq[:, None] * seq[None, :]
+
+
+@pytest.mark.parametrize("n,masked_last", [(1, False), (2, True), (3, False)])
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_triangle_multiplication_tiny(device, n, masked_last, outgoing, bf16):
+    announce("trimul tiny", n, masked_last, outgoing, bf16)
+    ref, hip = pair_of("TriangleMultiplication", dict(c_pair=128, _outgoing=outgoing), seed=n)
+    pair, mask = pair_case(n, n, masked_last)
+    if bf16:
+        pair = pair.bfloat16()
+    got, want = run_both(ref, hip, (pair.float(), mask), (pair.to(device), mask.to(device)), bf16)
+    check(got, want, bf16, "trimul tiny")
+
+
+@pytest.mark.parametrize("n,masked_last", [(1, False), (2, True), (3, False)])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_grid_self_attention_tiny(device, n, masked_last, transpose, bf16):
+    announce("grid attention tiny", n, masked_last, transpose, bf16)
+    ref, hip = pair_of("GridSelfAttention", dict(c_pair=128, num_head=4, transpose=transpose), seed=n + 1)
+    pair, mask = pair_case(n, n + 1, masked_last)
+    if bf16:
+        pair = pair.bfloat16()
+    got, want = run_both(ref, hip, (pair.float(), mask), (pair.to(device), mask.to(device)), bf16)
+    check(got, want, bf16, "grid attention tiny")
+
+
+@pytest.mark.parametrize("rows", [(1,), (1, 1), (3, 1)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_transition_tiny(device, rows, bf16):
+    announce("transition tiny", rows, bf16)
+    ref, hip = pair_of("Transition", dict(c_x=128, num_intermediate_factor=4), seed=5)
+    x = torch.randn(*rows, 128)
+    if bf16:
+        x = x.bfloat16()
+    got, want = run_both(ref, hip, (x.float(),), (x.to(device),), bf16)
+    check(got, want, bf16, "transition tiny")
+
+
+@pytest.mark.parametrize("q_len,k_len", [(1, 1), (1, 5), (4, 1), (2, 65)])
+@pytest.mark.parametrize("mask_rank", [None, 1, 2, 4])
+@pytest.mark.parametrize("d", [7, 24, 48])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_attention_edge_shapes(device, q_len, k_len, mask_rank, d, dtype):
+    """Single queries and keys, every mask rank of the reference's broadcast rules, batch-shared
+    bias; masks keep the first key so that no row is fully masked."""
+    announce("attention edges", q_len, k_len, mask_rank, d, dtype)
+    g = torch.Generator().manual_seed(q_len * 100 + k_len + d)
+    B, H = 2, 3
+    q = torch.randn(B, H, q_len, d, generator=g).to(dtype)
+    k = torch.randn(B, H, k_len, d, generator=g).to(dtype)
+    v = torch.randn(B, H, k_len, d, generator=g).to(dtype)
+    bias = torch.randn(H, q_len, k_len, generator=g).to(dtype)
+    keep = torch.rand(B, k_len, generator=g) > 0.4
+    keep[:, 0] = True
+    mask = None if mask_rank is None else keep[0] if mask_rank == 1 else keep if mask_rank == 2 \
+        else keep[:, None, None, :].expand(B, H, q_len, k_len).contiguous()
+    want = R.dot_product_attention(q.float(), k.float(), v.float(), mask, bias.float())
+    got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device),
+                                       None if mask is None else mask.to(device), bias.to(device))
+    check(got, want, dtype == torch.bfloat16, "attention edges")
+
+
+@pytest.mark.parametrize("n,samples", [(1, 1), (2, 3), (5, 1)])
+def test_diffusion_transformer_tiny(device, n, samples):
+    announce("diffusion transformer tiny", n, samples)
+    args = dict(c_act=256, c_single_cond=64, c_pair_cond=128, num_head=16, num_blocks=2, super_block_size=2)
+    ref, hip = pair_of("DiffusionTransformer", args, seed=n + samples, device=device)
+    g = torch.Generator().manual_seed(n)
+    act = torch.randn(samples, n, 256, generator=g).bfloat16()
+    mask = torch.ones(n)
+    scond, pcond = torch.randn(n, 64, generator=g), torch.randn(n, n, 128, generator=g)
+    with torch.inference_mode():
+        want = torch.stack([ref(act[s].float().clone(), mask, scond, pcond) for s in range(samples)])
+        with autocast(True):
+            got = hip(act.to(device).clone(), mask.to(device), scond.to(device), pcond.to(device))
+    assert torch.isfinite(got.float()).all()
+    assert_parity_bf16(got, want, "diffusion transformer tiny", stores=2 * args["num_blocks"])
