@@ -107,3 +107,27 @@ def test_diffusion_transformer_tiny(device, n, samples):
             got = hip(act.to(device).clone(), mask.to(device), scond.to(device), pcond.to(device))
     assert torch.isfinite(got.float()).all()
     assert_parity_bf16(got, want, "diffusion transformer tiny", stores=2 * args["num_blocks"])
+
+
+@pytest.mark.parametrize("module", ["TriangleMultiplication", "GridSelfAttention", "Transition"])
+def test_strided_inputs(device, module):
+    """Transposed (non-contiguous) pair and mask views give the result of their contiguous
+    copies."""
+    announce("strided inputs", module)
+    args = {"TriangleMultiplication": dict(c_pair=128, _outgoing=False),
+            "GridSelfAttention": dict(c_pair=128, num_head=4, transpose=True),
+            "Transition": dict(c_x=128, num_intermediate_factor=4)}[module]
+    ref, hip = pair_of(module, args, seed=9)
+    n = 37
+    g = torch.Generator().manual_seed(9)
+    base = torch.randn(n, n, 128, generator=g).bfloat16()
+    keep = (torch.rand(n, n, generator=g) > 0.2).float()
+    pair, mask = base.transpose(0, 1), keep.t()
+    dpair, dmask = base.to(device).transpose(0, 1), keep.to(device).t()
+    assert not dpair.is_contiguous() and not dmask.is_contiguous()
+    if module == "Transition":
+        ref_in, dev_in = (pair.float(),), (dpair,)
+    else:
+        ref_in, dev_in = (pair.float(), mask), (dpair, dmask)
+    got, want = run_both(ref, hip, ref_in, dev_in, True)
+    check(got, want, True, f"{module} strided")
