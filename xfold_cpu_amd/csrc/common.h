@@ -53,6 +53,14 @@ int device_cu_count(int *cus);
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t align_up(int64_t a, int64_t b) { return ceil_div(a, b) * b; }
+// Workgroups for a persistent kernel whose `per_wg` wavefronts take `units` work units
+// round-robin, at most one workgroup per CU: as few as give every wavefront the same number
+// of rounds as `cus` workgroups would (N=384 pair kernels: 192 or 231 instead of 256, 3% of
+// a block, with the weights each workgroup stages into LDS fetched fewer times).
+inline int64_t balanced_grid(int64_t units, int64_t per_wg, int cus) {
+  if (units <= 0) return 0;
+  return ceil_div(units, per_wg * ceil_div(units, per_wg * int64_t(cus)));
+}
 
 // Bump allocator over a caller-provided workspace; 256-byte aligned slices.
 struct Carver {

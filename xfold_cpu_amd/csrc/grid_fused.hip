@@ -321,7 +321,7 @@ int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {
   const int64_t units = int64_t(a.n) * (a.npad / 32);
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
+  const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
   KernelTimer timer("grid_project", s);
   if (pair_dtype == XFH_BF16)
     grid_project_kernel<bf16><<<grid, 512, 0, s>>>(a);
@@ -334,7 +334,7 @@ int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStrea
   const int64_t steps = ceil_div(int64_t(a.n) * a.n, 16);
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(steps, 8))));
+  const dim3 grid(unsigned(balanced_grid(steps, 8, cus)));
   KernelTimer timer("grid_output", s);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
     grid_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);

@@ -105,7 +105,7 @@ int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s) {
   if (units == 0) return XFH_OK;
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
+  const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
   KernelTimer timer("pair_bias", s);
   if (pair_dtype == XFH_BF16)
     pair_bias_kernel<bf16><<<grid, 512, 0, s>>>(a);

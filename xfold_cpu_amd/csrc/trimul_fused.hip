@@ -300,7 +300,7 @@ int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
   const int64_t units32 = int64_t(a.n) * (a.ld / 32);
   const bool wide = units32 >= int64_t(cus) * 8 * 4;
   const int64_t units = wide ? units32 : 2 * units32;
-  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(units, 8))));
+  const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
   KernelTimer timer("trimul_project", s);
   if (pair_dtype == XFH_BF16) {
     if (wide) trimul_project_kernel<bf16, 2><<<grid, 512, 0, s>>>(a);
@@ -318,7 +318,7 @@ int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStre
     return fail(XFH_EINVAL, "trimul_output: result planes overlap or are not 16-byte aligned");
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  const dim3 grid(unsigned(std::min<int64_t>(cus, ceil_div(steps, 8))));
+  const dim3 grid(unsigned(balanced_grid(steps, 8, cus)));
   KernelTimer timer("trimul_output", s);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
     trimul_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
