@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 5
+#define XFH_ABI_VERSION 6
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -130,6 +130,12 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
                               void *out, int out_dtype, const int64_t *shape, const int64_t *strides,
                               float scale, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* Largest key count (and token count N) the pipelined attention kernel takes: the limit of
+ * a packed bias (xfh_attention_bias_pack, xfh_pair_attention_bias). Longer key sequences
+ * take xfh_dot_product_attention's general kernel with an unpacked bias. Capability query
+ * with no counterpart in the reference, which has no such limit. */
+int64_t xfh_attention_max_keys(void);
 
 /* Converts G attention biases, bias[g][h][q][k] (shape = {G, H, Q, K}, strides in
  * elements, f32 or bf16), into the pipelined attention kernel's layout once:

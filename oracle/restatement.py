@@ -210,6 +210,31 @@ class GridSelfAttention(nn.Module):
         return out
 
 
+def grid_self_attention_rows(module: "GridSelfAttention", pair: torch.Tensor, mask: torch.Tensor,
+                             rows: torch.Tensor, attention=None) -> torch.Tensor:
+    """Batch rows ``rows`` of ``GridSelfAttention.forward`` (``xfold/nn/attention.py:80-105``)
+    without evaluating the others: the starting node's output pair rows ``out[rows]``, the
+    ending node's output pair columns ``out[:, rows]`` returned as ``[len(rows), n, c]``.
+
+    Batch rows are independent once the bias (from the whole normalised pair, :89-95) is
+    known: each row's q/k/v/gate come from that row of the (transposed) input (:97-100),
+    and its 2-D mask row is ``mask[row]`` (``xfold/fastnn/attention.py:57-61``). Used at
+    sizes where evaluating every row on the host would take minutes.
+    """
+    attention = attention or dot_product_attention
+    normed = module.act_norm(pair)
+    bias = module.pair_bias_projection(normed).permute(2, 0, 1)
+    if module.transpose:
+        normed = normed.permute(1, 0, 2)
+    x = normed[rows]
+    q = _heads_first(module.q_projection(x), module.num_head)
+    k = _heads_first(module.k_projection(x), module.num_head)
+    v = _heads_first(module.v_projection(x), module.num_head)
+    weighted = _heads_last(attention(q, k, v, mask=mask[rows], bias=bias))
+    weighted *= torch.sigmoid(module.gating_query(x))
+    return module.output_projection(weighted)
+
+
 class Transition(nn.Module):
     """``xfold/nn/primitives.py:20-37``: LN -> GLU(transition1.weight.T) -> transition2."""
 

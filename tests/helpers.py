@@ -52,47 +52,38 @@ def assert_parity(actual, expected, tol, what=""):
     return err
 
 
-def bf16_half_ulp(x: torch.Tensor) -> torch.Tensor:
-    """Half a bf16 unit in the last place at |x| (8 significant bits)."""
-    ax = x.abs().clamp_min(2.0 ** -126)
-    return torch.pow(2.0, torch.floor(torch.log2(ax)) - 8)
+# bf16 mode. The north-star bar (2e-2 of the output RMS) applies to the RMS of the error.
+# The max error must stay within the larger of that same 2e-2 and 1.5x the max error of the
+# case's bf16 floor: the same oracle evaluation, on the same inputs, exact except for the
+# roundings the bf16 dtype contract itself imposes (oracle.bf16_floor.Bf16Operands): every
+# matrix product's operands rounded to bf16, a bf16 residual stream rounded after each
+# update (mark_residual), and a bf16 output rounded once (stored=True). That floor is
+# 2-7e-2 on the pair operators, above the literal bar, while its RMS error is ~5e-3. A case
+# without a floor is held to 2e-2.
+FLOOR_FACTOR = 1.5
 
 
-def stored_rel_err(actual: torch.Tensor, expected: torch.Tensor, stores: float = 1.0) -> float:
-    """max(|a - e| - stores * half_ulp_bf16) / RMS(e): the error of a bf16-stored result
-    with the rounding of its `stores` bf16 stores excluded (and nothing else).
-
-    Rounding the exact fp32 answer to bf16 alone gives max|d|/RMS of 1.3e-2..2.7e-2 on
-    this path's outputs, and the reference's own bf16 path 3.8e-2..9.7e-2, so the
-    literal max-abs bar on bf16-stored values would measure the storage format.
-    """
-    a = actual.detach().to(torch.float64).cpu()
-    e = expected.detach().to(torch.float64).cpu()
-    assert a.shape == e.shape, (a.shape, e.shape)
-    if e.numel() == 0:
-        return 0.0
-    slack = bf16_half_ulp(torch.maximum(a.abs(), e.abs())) * stores
-    excess = ((a - e).abs() - slack).clamp_min(0.0)
-    rms = math.sqrt(float((e * e).mean()))
-    err = float(excess.max())
-    if not math.isfinite(float((a - e).abs().max())):
-        return math.inf
-    return err / rms if rms > 0 else err
+def bf16_stored(t):
+    """``t`` (a tensor or a tuple of them) rounded to bf16, as a bf16 output store does."""
+    if isinstance(t, (tuple, list)):
+        return type(t)(bf16_stored(x) for x in t)
+    return None if t is None else t.detach().to(torch.bfloat16).to(t.dtype)
 
 
-def assert_stored_parity(actual, expected, tol, what="", stores=1.0):
-    err = stored_rel_err(actual, expected, stores)
-    assert err <= tol, f"{what}: store-aware max|diff|/rms = {err:.3e} > {tol:.1e}"
-    return err
+def floor_of(fn, stored=False):
+    """fn() (an oracle evaluation on the CPU) under Bf16Operands; ``stored`` also rounds
+    the result to bf16 (a module whose output is stored in bf16)."""
+    from oracle.bf16_floor import Bf16Operands
+    with torch.inference_mode(), Bf16Operands():
+        out = fn()
+    return bf16_stored(out) if stored else out
 
 
-# bf16 mode. The north-star bar (2e-2 of the output RMS) is applied to the RMS of the
-# error; the max-abs error gets a guard of 8e-2 instead, because an exact computation
-# whose only rounding is bf16 matmul operands (oracle/bf16_floor.py) already has
-# max|d|/RMS of 2.3e-2 (Transition), 3.4e-2 (TriangleMultiplication) and 4.1e-2
-# (GridSelfAttention) at N=64, while its RMS error is ~5e-3. The guard still fails any
-# element-level mistake (a wrong index or mask gives O(1) errors).
-TOL_BF16_MAX = 8e-2
+def residual(t):
+    """A bf16 residual stream for the floor: ``t`` as an fp32 tensor whose in-place updates
+    Bf16Operands rounds to bf16."""
+    from oracle.bf16_floor import mark_residual
+    return mark_residual(t)
 
 
 def rms_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
@@ -106,12 +97,16 @@ def rms_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     return num / den if den > 0 else num
 
 
-def assert_parity_bf16(actual, expected, what="", stores=0.0):
-    """bf16-mode parity: RMS error <= TOL_BF16 and max error (bf16 store rounding of
-    `stores` stores excluded) <= TOL_BF16_MAX, both relative to RMS(expected)."""
+def assert_parity_bf16(actual, expected, what="", floor=None):
+    """bf16-mode parity, relative to RMS(expected): RMS error <= TOL_BF16, and max error
+    <= max(TOL_BF16, FLOOR_FACTOR x the max error of `floor`, the case's bf16 floor)."""
     rms_err = rms_rel_err(actual, expected)
-    max_err = stored_rel_err(actual, expected, stores) if stores else rel_err(actual, expected)
-    print(f"[parity] {what}: rms {rms_err:.3e} max {max_err:.3e}", flush=True)
+    max_err = rel_err(actual, expected)
+    floor_err = rel_err(floor, expected) if floor is not None else 0.0
+    guard = max(TOL_BF16, FLOOR_FACTOR * floor_err)
+    print(f"[parity] {what}: rms {rms_err:.3e} max {max_err:.3e} floor {floor_err:.3e} "
+          f"guard {guard:.3e}", flush=True)
     assert rms_err <= TOL_BF16, f"{what}: rms|diff|/rms = {rms_err:.3e} > {TOL_BF16:.1e}"
-    assert max_err <= TOL_BF16_MAX, f"{what}: max|diff|/rms = {max_err:.3e} > {TOL_BF16_MAX:.1e}"
+    assert max_err <= guard, (f"{what}: max|diff|/rms = {max_err:.3e} > {guard:.3e} "
+                              f"(floor {floor_err:.3e})")
     return rms_err, max_err

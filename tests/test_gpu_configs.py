@@ -1,0 +1,222 @@
+"""Parity at every benchmark configuration's own workload (xfold_cpu_amd.synthetic.CONFIGS),
+built exactly as bench.py builds it: the same seeded weights (block b initialised with seed
+b, LayerNorm gamma = 1, beta = 0), the same seeded activations and masks, bf16 activations
+under CUDA bf16 autocast for C2-C5 and fp32 without autocast for C1. Each case is checked
+against the fp32 CPU oracle (oracle/restatement.py) on the same inputs, and each bf16 case's
+max error against its bf16 floor (the same oracle evaluation with bf16-rounded
+matrix-product operands, the bf16 residual stream or output rounded as the HIP path
+stores it; tests/helpers.py).
+
+  C1  PairformerBlock pair stack, fp32, N=128                 xfold/nn/pairformer.py:77-100
+  C2  PairformerBlock pair stack, bf16, N=384, 32 padded      xfold/nn/pairformer.py:77-100
+  C3  PairformerBlock with single track, bf16, N=768, 77 padded (one trunk block), and the
+      trunk's block-after-block loop (xfold/alphafold3.py:262-264) at a smaller N
+  C4  DiffusionTransformer, 24 blocks, c=768, 16x48, 5 samples, N=768
+                                                              xfold/nn/diffusion_transformer.py:250-272
+  C5  the pair block's ops at N=1536 with 77 random padded tokens: both triangle
+      multiplications and the transition in full, both triangle-attention nodes on a
+      sample of batch rows (every row is computed on the GPU; the oracle evaluates the
+      sampled rows, oracle.restatement.grid_self_attention_rows)
+
+The host oracle takes 5-40 s per case (twice: exact and floor)."""
+
+import pytest
+import torch
+
+from oracle import restatement as R
+from tests.helpers import TOL_FP32, assert_parity, assert_parity_bf16, floor_of, residual
+from tests.test_gpu_ops import announce, autocast
+from xfold_cpu_amd import nn as hnn
+from xfold_cpu_amd.synthetic import CONFIGS, diffusion_inputs, init_module_, pair_block_inputs
+
+pytestmark = [pytest.mark.gpu, pytest.mark.timeout(600)]
+
+BLOCK_ARGS = dict(n_heads=16, c_pair=128, c_single=384, n_heads_pair=4)
+
+
+def chunked_attention(*args, **kwargs):
+    return R.dot_product_attention_chunked(*args, rows_per_chunk=32, **kwargs)
+
+
+def bench_blocks(cfg, device, count=1):
+    """(oracle block, HIP block) pairs with bench.py's weights: block b seeded with b."""
+    pairs = []
+    for b in range(count):
+        ref = init_module_(R.PairformerBlock(**BLOCK_ARGS, with_single=cfg["with_single"]).eval(), seed=b)
+        hip = hnn.PairformerBlock(**BLOCK_ARGS, with_single=cfg["with_single"]).eval()
+        hip.load_state_dict(ref.state_dict())
+        pairs.append((ref, hip.to(device)))
+    return pairs
+
+
+def bench_inputs(cfg, n=None, pad=None):
+    return pair_block_inputs(n or cfg["n"], pad=cfg["pad"] if pad is None else pad,
+                             random_pad=cfg["random_pad"], seed=0, with_single=cfg["with_single"])
+
+
+def test_c1_pair_block_fp32(device):
+    cfg = CONFIGS["C1"]
+    announce("C1 pair block fp32", cfg["n"])
+    [(ref, hip)] = bench_blocks(cfg, device)
+    inp = bench_inputs(cfg)
+    with torch.inference_mode():
+        want = ref(inp.pair.clone(), inp.pair_mask)
+        got = hip(inp.pair.to(device).contiguous(), inp.pair_mask.to(device))
+    assert got.dtype == torch.float32
+    assert_parity(got, want, TOL_FP32, "C1 pair block")
+
+
+def test_c2_pair_block(device):
+    cfg = CONFIGS["C2"]
+    announce("C2 pair block bf16", cfg["n"], "pad", cfg["pad"])
+    [(ref, hip)] = bench_blocks(cfg, device)
+    inp = bench_inputs(cfg)
+    pair = inp.pair.bfloat16()
+
+    def oracle(wrap=lambda t: t):
+        return ref(wrap(pair.float()), inp.pair_mask, attention=chunked_attention)
+    with torch.inference_mode():
+        with autocast(True):
+            got = hip(pair.to(device).contiguous(), inp.pair_mask.to(device))
+        want = oracle()
+    # bf16 residual stream, rounded at each of its 5 in-place updates (so is the floor's).
+    floor = floor_of(lambda: oracle(residual))
+    assert torch.isfinite(got.float()).all()
+    assert_parity_bf16(got, want, "C2 pair block N=384", floor=floor)
+
+
+def test_c3_block_with_single_track(device):
+    cfg = CONFIGS["C3"]
+    announce("C3 block with single track bf16", cfg["n"], "pad", cfg["pad"])
+    [(ref, hip)] = bench_blocks(cfg, device)
+    inp = bench_inputs(cfg)
+    pair, single = inp.pair.bfloat16(), inp.single.bfloat16()
+
+    def oracle(wrap=lambda t: t):
+        return ref(wrap(pair.float()), inp.pair_mask, wrap(single.float()), inp.seq_mask,
+                   attention=chunked_attention)
+    with torch.inference_mode():
+        with autocast(True):
+            got_pair, got_single = hip(pair.to(device).contiguous(), inp.pair_mask.to(device),
+                                       single.to(device).contiguous(), inp.seq_mask.to(device))
+        want_pair, want_single = oracle()
+    floor_pair, floor_single = floor_of(lambda: oracle(residual))
+    assert torch.isfinite(got_pair.float()).all() and torch.isfinite(got_single.float()).all()
+    assert_parity_bf16(got_pair, want_pair, "C3 block N=768 pair", floor=floor_pair)
+    assert_parity_bf16(got_single, want_single, "C3 block N=768 single", floor=floor_single)
+
+
+def test_c3_trunk_loop(device):
+    """Three trunk blocks in sequence (xfold/alphafold3.py:262-264), each seeing the previous
+    block's pair and single, at N=160 with the C3 padding fraction (16 tokens)."""
+    cfg = CONFIGS["C3"]
+    n, blocks = 160, 3
+    announce("C3 trunk loop", n, blocks)
+    pairs = bench_blocks(cfg, device, count=blocks)
+    inp = bench_inputs(cfg, n=n, pad=16)
+    pair, single = inp.pair.bfloat16(), inp.single.bfloat16()
+
+    def oracle(wrap=lambda t: t):
+        p, s = wrap(pair.float()), wrap(single.float())
+        for ref, _ in pairs:
+            p, s = ref(p, inp.pair_mask, s, inp.seq_mask)
+        return p, s
+    with torch.inference_mode():
+        dp, ds = pair.to(device).contiguous(), single.to(device).contiguous()
+        with autocast(True):
+            for _, hip in pairs:
+                hip(dp, inp.pair_mask.to(device), ds, inp.seq_mask.to(device))
+        want_pair, want_single = oracle()
+    floor_pair, floor_single = floor_of(lambda: oracle(residual))
+    assert_parity_bf16(dp, want_pair, "C3 trunk loop pair", floor=floor_pair)
+    assert_parity_bf16(ds, want_single, "C3 trunk loop single", floor=floor_single)
+
+
+def test_c4_diffusion_transformer(device):
+    cfg = CONFIGS["C4"]
+    announce("C4 diffusion transformer", cfg["n"], cfg["samples"], cfg["blocks"])
+    ref = init_module_(R.DiffusionTransformer().eval(), seed=0)
+    hip = hnn.DiffusionTransformer().eval()
+    hip.load_state_dict(ref.state_dict())
+    hip.to(device)
+    inp = diffusion_inputs(cfg["n"], samples=cfg["samples"])
+    act = inp.act.bfloat16()
+
+    def oracle(wrap=lambda t: t):
+        return torch.stack([ref(wrap(act[s].float()), inp.mask, inp.single_cond, inp.pair_cond)
+                            for s in range(cfg["samples"])])
+    with torch.inference_mode():
+        with autocast(True):
+            got = hip(act.to(device).clone(), inp.mask.to(device), inp.single_cond.to(device),
+                      inp.pair_cond.to(device))
+        want = oracle()
+    # act is a bf16 residual stream rounded at each of its 2 updates per block.
+    floor = floor_of(lambda: oracle(residual))
+    assert torch.isfinite(got.float()).all()
+    assert_parity_bf16(got, want, "C4 diffusion transformer", floor=floor)
+
+
+@pytest.fixture(scope="module")
+def c5(device):
+    """C5 inputs and bench.py's block-0 weights; the ops run on the same bf16 pair."""
+    cfg = CONFIGS["C5"]
+    [(ref, hip)] = bench_blocks(cfg, device)
+    inp = bench_inputs(cfg)
+    pair = inp.pair.bfloat16()
+    return dict(ref=ref, hip=hip, pair=pair, mask=inp.pair_mask, dpair=pair.to(device).contiguous(),
+                dmask=inp.pair_mask.to(device), seq=inp.seq_mask)
+
+
+@pytest.mark.parametrize("name", ["triangle_multiplication_outgoing", "triangle_multiplication_incoming"])
+def test_c5_triangle_multiplication(c5, name):
+    announce("C5", name, c5["pair"].shape[0])
+    ref, hip = getattr(c5["ref"], name), getattr(c5["hip"], name)
+
+    def oracle():
+        return ref(c5["pair"].float(), c5["mask"])
+    with torch.inference_mode():
+        with autocast(True):
+            got = hip(c5["dpair"], c5["dmask"]).float().cpu()
+        want = oracle()
+    floor = floor_of(oracle, stored=True)
+    assert torch.isfinite(got).all()
+    assert_parity_bf16(got, want, f"C5 {name} N=1536", floor=floor)
+
+
+@pytest.mark.parametrize("name", ["pair_attention1", "pair_attention2"])
+def test_c5_triangle_attention(c5, name):
+    """Every batch row is computed on the GPU; 40 rows are checked: 32 random ones, two
+    padded ones (fully masked: uniform over all keys) and the first and last rows."""
+    n = c5["pair"].shape[0]
+    announce("C5", name, n)
+    ref, hip = getattr(c5["ref"], name), getattr(c5["hip"], name)
+    g = torch.Generator().manual_seed(5)
+    padded = torch.nonzero(c5["seq"] == 0).flatten()
+    rows = torch.cat([torch.randperm(n, generator=g)[:32], padded[:2], torch.tensor([0, n - 1])])
+    rows = torch.unique(rows)
+
+    def oracle():
+        return R.grid_self_attention_rows(ref, c5["pair"].float(), c5["mask"], rows)
+    with torch.inference_mode():
+        with autocast(True):
+            out = hip(c5["dpair"], c5["dmask"])
+        out = out.permute(1, 0, 2) if ref.transpose else out
+        got = out[rows.to(out.device)].float().cpu()
+        want = oracle()
+    floor = floor_of(oracle, stored=True)
+    assert torch.isfinite(got).all()
+    assert_parity_bf16(got, want, f"C5 {name} N=1536 ({len(rows)} rows)", floor=floor)
+
+
+def test_c5_transition(c5):
+    announce("C5 pair transition", c5["pair"].shape[0])
+    ref, hip = c5["ref"].pair_transition, c5["hip"].pair_transition
+
+    def oracle():
+        return ref(c5["pair"].float())
+    with torch.inference_mode():
+        with autocast(True):
+            got = hip(c5["dpair"]).float().cpu()
+        want = oracle()
+    floor = floor_of(oracle, stored=True)
+    assert_parity_bf16(got, want, "C5 pair transition N=1536", floor=floor)

@@ -334,6 +334,8 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   return attention(a, dtype, as_stream(stream));
 }
 
+int64_t xfh_attention_max_keys(void) { return grid_attention_max_n(); }
+
 int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides,
                             void *packed, void *stream) {
   XFH_REQUIRE(shape && strides, "attention_bias_pack: null shape/strides");

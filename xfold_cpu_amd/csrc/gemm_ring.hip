@@ -251,7 +251,6 @@ bool aligned(const void *ptr, int bytes) { return reinterpret_cast<uintptr_t>(pt
 }  // namespace
 
 // Ring configurations (tile width, k-step, stages, workgroups per CU).
-using RingWide = Ring<128, 64, 2, 2>;     // wide outputs, k % 64 == 0
 using RingMid = Ring<96, 64, 2, 2>;       // 3/4-width tiles: more workgroups for narrow outputs
 using RingNarrow = Ring<64, 64, 3, 2>;    // N <= 64, or too few workgroups otherwise
 using RingShallow = Ring<128, 32, 4, 2>;  // k % 64 != 0
@@ -280,7 +279,7 @@ template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dty
   return check_launch("gemm_ring");
 }
 
-enum class RingPick { Wide, Mid, Narrow, Shallow, ShallowNarrow, XWide };
+enum class RingPick { Mid, Narrow, Shallow, ShallowNarrow, XWide };
 
 // Tile width: the 64-column tile (the only one with a 3-stage ring at two workgroups per
 // CU) unless the grid then needs more rounds of workgroups than a wider tile would, rounds
@@ -288,7 +287,9 @@ enum class RingPick { Wide, Mid, Narrow, Shallow, ShallowNarrow, XWide };
 // 64-column tile is fastest whenever it fits in one round, the 96-column tile on
 // 3840 x 2304 outputs; the 192-column tile wherever it needs one round fewer: the diffusion
 // QKV Linear and GLU, 0.5% and 1.9% of a diffusion transformer). 64-deep k-steps when k
-// allows. GLU pairs whole 32-column groups per wavefront, so it takes 64, 128 or 192.
+// allows. GLU pairs whole 32-column groups per wavefront, so it takes 64 or 192. A
+// 128-column tile with 64-deep steps never wins this cost: a 128-column grid needs at
+// least half the rounds of the 64-column one, so it is not built.
 RingPick pick_ring(const GemmArgs &p, int64_t batch, bool glu, int cus) {
   const int64_t mt = ceil_div(p.M, 128) * batch, slots = 2 * int64_t(cus);
   auto rounds = [&](int bn) { return ceil_div(mt * ceil_div(p.N, bn), slots); };
@@ -299,10 +300,6 @@ RingPick pick_ring(const GemmArgs &p, int64_t batch, bool glu, int cus) {
   if (!glu && rounds(96) * 96 <= cost) {
     best = RingPick::Mid;
     cost = rounds(96) * 96;
-  }
-  if (rounds(128) * 128 < cost) {
-    best = RingPick::Wide;
-    cost = rounds(128) * 128;
   }
   if (p.N % 192 == 0 && rounds(192) * 192 <= cost) best = RingPick::XWide;
   return best;
@@ -321,16 +318,21 @@ int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStre
   XFH_TRY(device_cu_count(&cus));
   KernelTimer timer("gemm_ring", s);
   const RingPick pick = pick_ring(p, batch, glu, cus);
-  const int bn = pick == RingPick::XWide ? 192
-                 : pick == RingPick::Wide || pick == RingPick::Shallow ? 128 : pick == RingPick::Mid ? 96 : 64;
+  const int bn = pick == RingPick::XWide ? 192 : pick == RingPick::Shallow ? 128 : pick == RingPick::Mid ? 96 : 64;
   // Per-XCD row runs when row blocks span several tiles, the whole B operand fits comfortably
   // in one XCD's 4 MB L2 and the grid covers every CU (measured: 8% on 3840 x 768 outputs;
   // slower when B crowds the L2 or a row block is one tile).
   GemmArgs q = p;
   q.xcd_rows = !glu && p.K % 64 == 0 && int64_t(p.N) * p.K * 2 <= (int64_t(5) << 19) && p.N > bn &&
                ceil_div(p.M, 128) * ceil_div(p.N, bn) >= cus;
+  // The configuration is observable through the kernel timer of that name.
+  static const char *const names[5][2] = {{"gemm_ring.mid", "gemm_ring.mid+xcd"},
+                                          {"gemm_ring.narrow", "gemm_ring.narrow+xcd"},
+                                          {"gemm_ring.shallow", "gemm_ring.shallow+xcd"},
+                                          {"gemm_ring.shallow_narrow", "gemm_ring.shallow_narrow+xcd"},
+                                          {"gemm_ring.xwide", "gemm_ring.xwide+xcd"}};
+  KernelTimer config_timer(names[int(pick)][q.xcd_rows ? 1 : 0], s);
   switch (pick) {
-    case RingPick::Wide: return launch_ring<RingWide>(q, batch, out_dtype, glu, s);
     case RingPick::Mid: return launch_ring<RingMid>(q, batch, out_dtype, glu, s);
     case RingPick::XWide: return launch_ring<RingXWide>(q, batch, out_dtype, glu, s);
     case RingPick::Narrow: return launch_ring<RingNarrow>(q, batch, out_dtype, glu, s);

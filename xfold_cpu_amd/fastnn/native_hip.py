@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, BF16, BOOL = 0, 1, 2
 BIAS_PACKED = 3                 # bias 'dtype' of a block written by xfh_attention_bias_pack
@@ -53,6 +53,7 @@ SIGNATURES = {
     "xfh_gated_linear_unit": (_i, [_p, _p, _i64, _i64, _i64, _i, _p, _i, _p]),
     "xfh_dot_product_attention_workspace_size": (_i64, [_pi64, _i]),
     "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _pi64, _pi64, _f, _p, _i64, _p]),
+    "xfh_attention_max_keys": (_i64, []),
     "xfh_attention_bias_pack": (_i, [_p, _i, _pi64, _pi64, _p, _p]),
     "xfh_pair_attention_bias": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _i64, _p, _p]),
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
@@ -111,6 +112,12 @@ def kernel_timing_read(name: str):
     total, count = ctypes.c_double(), ctypes.c_int64()
     call("xfh_kernel_timing_read", name.encode(), ctypes.byref(total), ctypes.byref(count))
     return total.value, count.value
+
+
+@functools.lru_cache(maxsize=None)
+def attention_max_keys() -> int:
+    """Largest key count of the pipelined attention kernel, hence of a packed bias."""
+    return int(load_library().xfh_attention_max_keys())
 
 
 def runtime_info() -> str:

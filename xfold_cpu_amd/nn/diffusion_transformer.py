@@ -225,8 +225,12 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
     if mask is not None and mask.dtype not in (torch.bool, torch.uint8):
         mask = mask.to(torch.bool)      # once, not per block (xfold/fastnn/attention.py:57-61)
     n_blocks = module.num_super_blocks * size
-    if dtype == torch.bfloat16 and act.shape[-1] // heads <= 64 and pair_cond.shape[-1] == 128 and \
-            n_blocks * heads <= 384 and tuple(ln.normalized_shape) == (128,):
+    # A packed bias (either path below) feeds the pipelined attention kernel, which takes
+    # bf16, head dims <= 64 and at most attention_max_keys() keys.
+    packed_bias = dtype == torch.bfloat16 and act.shape[-1] // heads <= 64 and \
+        pair_cond.shape[0] <= nh.attention_max_keys()
+    if packed_bias and pair_cond.shape[-1] == 128 and n_blocks * heads <= 384 and \
+            tuple(ln.normalized_shape) == (128,):
         # Every super-block's pair logits in one pass over pair_cond, straight into the
         # attention kernel's bias layout; block b reads heads b*H .. b*H + H - 1.
         projs = [module.pair_logits_projection[s].weight for s in range(module.num_super_blocks)]
@@ -243,7 +247,6 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         return act
     pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
                               out_dtype=dtype, owner=ln)
-    packed_bias = dtype == torch.bfloat16 and act.shape[-1] // heads <= 64
     for s in range(module.num_super_blocks):
         weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
         logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]

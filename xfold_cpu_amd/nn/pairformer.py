@@ -24,13 +24,13 @@ from .triangle_multiplication import TriangleMultiplication, triangle_multiplica
 
 
 def pair_logits_hip(block: nn.Module, pair: torch.Tensor, dtype: torch.dtype):
-    """``Linear(LN(pair)).permute(2, 0, 1)`` (``pairformer.py:103-106``): with bf16 compute
-    and 128 pair channels one kernel writes it as the attention's packed bias
-    (:class:`ops.PackedBias`), else a [H, N, N] view."""
+    """``Linear(LN(pair)).permute(2, 0, 1)`` (``pairformer.py:103-106``): with bf16 compute,
+    128 pair channels and at most ``attention_max_keys()`` tokens one kernel writes it as the
+    attention's packed bias (:class:`ops.PackedBias`), else a [H, N, N] view."""
     norm = block.single_pair_logits_norm
     proj = block.single_pair_logits_projection
     if dtype == torch.bfloat16 and pair.shape[-1] == 128 and proj.weight.shape[0] <= 384 \
-            and tuple(norm.normalized_shape) == (128,):
+            and tuple(norm.normalized_shape) == (128,) and pair.shape[0] <= nh.attention_max_keys():
         w = nh.linear_weight(block, "single_pair_logits_projection", dtype)
         return ops.PackedBias(ops.pair_attention_bias(pair, norm.weight, norm.bias, norm.eps, w, owner=norm))
     normed = ops.layer_norm(pair, norm.normalized_shape, norm.weight, norm.bias, norm.eps,
