@@ -1,6 +1,6 @@
 """Benchmark of the HIP Pairformer path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config C2] [--no-cpu-baseline]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config C2] [--no-cpu-baseline] [--no-c3]
 
 A step is one forward pass of the configured workload over synthetic inputs already in
 HBM: C2 (default, the metric's N=384 configuration) = one Pairformer pair block at N=384
@@ -8,9 +8,12 @@ in bf16; C1 = the same at N=128 in fp32; C3 = the 48-block trunk at N=768 (singl
 included); C4 = the 24-block diffusion transformer, 5 samples, N=768; C5 = one pair block
 at N=1536. ``value`` is milliseconds per Pairformer block (per transformer pass for C4).
 
-Rank 0 prints one JSON line with the driver's fields plus ``roofline`` (the dominant
-kernel, timed with HIP events on its own stream inside this run) and ``cpu_baseline``
-(the CPU oracle, a restatement of the reference's torch backend, on a bounded sample).
+One JSON line with the driver's fields plus ``roofline`` (the dominant kernel, timed with
+HIP events on its launch stream inside this run; ``traffic`` from the rocprofv3 counter
+record of the same kernel sources), ``kernels`` (every pair kernel's rate), ``c3`` (the
+48-block N=768 trunk timed in the same run, with its own roofline, when the configuration
+is the default C2) and ``cpu_baseline`` (restatements of the reference's torch and cpp
+backends timed on the host cores: 1 warm-up, median of 3).
 """
 
 from __future__ import annotations
@@ -32,7 +35,7 @@ PEAK_HBM_GBS = 8000.0
 
 
 # (timed steps, warm-up steps) per configuration; a step is one forward of the workload.
-DEFAULT_STEPS = {"C1": (200, 50), "C2": (200, 50), "C3": (10, 3), "C4": (10, 3), "C5": (20, 5)}
+DEFAULT_STEPS = {"C1": (200, 50), "C2": (200, 50), "C3": (5, 2), "C4": (10, 3), "C5": (20, 5)}
 
 
 def parse():
@@ -43,6 +46,8 @@ def parse():
     p.add_argument("--warmup", type=int, default=None)
     p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-c3", action="store_true",
+                   help="with the default C2 configuration, skip the 48-block C3 trunk timed beside it")
     p.add_argument("--graph", action="store_true",
                    help="capture one step in a HIP graph after the warm-up and time its replays")
     p.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -117,11 +122,32 @@ def build_workload(cfg_name, device):
     return step, 1, workload, cfg
 
 
-# HBM bytes per grid_attention_kernel launch, from rocprofv3 FETCH_SIZE and WRITE_SIZE passes over
-# the same workload (bench.py --config C2|C3 --copy-calibration-mb 512), calibrated against that
-# 512 MiB read+write kernel: bytes = (2 x FETCH_SIZE + WRITE_SIZE) KiB x 1024. Counters cannot be
-# read inside this process, so the figure is the recorded measurement for the configuration.
-ATTENTION_TRAFFIC_BYTES = {384: 168.25e6, 768: 1037.9e6}
+COUNTER_FILES = {384: ROOT / "profiles" / "counters_c2_n384.md", 768: ROOT / "profiles" / "counters_c3_n768.md"}
+
+
+def attention_traffic(n):
+    """HBM bytes per grid_attention_kernel launch at N tokens, from the rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes recorded in profiles/counters_*.md (calibrated against a 512 MiB
+    read+write kernel in the same run). Counters cannot be read inside this process, so the
+    figure is the recorded measurement; it is returned only while the attention kernel's
+    sources hash to the digest recorded with it, else (None, reason)."""
+    import hashlib
+    path = COUNTER_FILES.get(n)
+    if path is None or not path.exists():
+        return None, f"no counter record for N={n}"
+    rec = None
+    for line in path.read_text().splitlines():
+        if line.startswith('{"counters": "grid_attention_kernel"'):
+            rec = json.loads(line)
+    if rec is None:
+        return None, f"{path.name} holds no machine-readable record"
+    h = hashlib.sha256()
+    for src in rec["sources"]:
+        h.update((ROOT / src).read_bytes())
+    if h.hexdigest() != rec["sources_sha256"]:
+        return None, (f"stale: {path.name} was measured at commit {rec['commit']} on other attention "
+                      "kernel sources")
+    return rec["traffic_bytes"], f"{path.name} (commit {rec['commit']}, sources match)"
 
 
 PAIR_TIMERS = ("transition", "trimul_project", "trimul_contract", "trimul_output", "grid_project",
@@ -163,44 +189,167 @@ def kernel_roofline(step, n, steps):
     heads, d = 4, 32
     flops = 4.0 * n * heads * n * n * d            # Q.K^T and P.V over all N^3 logits
     achieved = flops / (ms * 1e-3) / 1e12
+    traffic, traffic_src = attention_traffic(n)
     return {"kernel": "grid_attention_kernel (triangle attention core)", "bound": "mfma",
             "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": ATTENTION_TRAFFIC_BYTES.get(n),
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
             "avg_launch_ms": round(ms, 4), "launches": launches, "flops_per_launch": flops,
             "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}, kernels
 
 
-def cpu_baseline(cfg, budget_s=30.0):
-    """The CPU oracle (restatement of the reference's torch backend) on the host cores:
-    one Pairformer pair block at the configuration's N under CPU bf16 autocast (fp32 for
-    C1), or the largest N in {N, 256, 128} whose single run fits the time budget."""
+def host_cpu():
+    """CPU model, sockets, cores and SMT of the host (lscpu), and the cores this process may use."""
+    import subprocess
+    info = {"affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+    except (OSError, subprocess.SubprocessError):
+        out = ""
+    keys = {"Model name": "model", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "CPU(s)": "cpus"}
+    for line in out.splitlines():
+        key, _, value = line.partition(":")
+        if key.strip() in keys:
+            value = value.strip()
+            info[keys[key.strip()]] = int(value) if value.isdigit() else value
+    return info
+
+
+def cpu_threads():
+    """Threads for the CPU legs: every core of this process's affinity, capped at the host share
+    the job was given (OMP_NUM_THREADS, set to one GPU's share of the box's cores)."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    share = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(affinity, int(share))) if share.isdigit() else affinity
+
+
+def _median_ms(fn, runs=3, warmup=1):
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append((time.perf_counter() - t0) * 1e3)
+    times.sort()
+    return times[len(times) // 2], [round(t, 1) for t in times]
+
+
+def cpu_workload(cfg_name, leg):
+    """(callable, description, blocks per call, extrapolation factor) of the CPU restatement of
+    one configuration. ``leg`` "torch": oracle.restatement (the reference's torch backend);
+    "cpp": oracle.cpp_port (the af3_kernels algorithms, OpenMP tiles over ATen GEMMs)."""
     import torch
     from oracle import restatement as R
-    from xfold_cpu_amd.synthetic import init_module_, pair_block_inputs
+    from xfold_cpu_amd.synthetic import CONFIGS, diffusion_inputs, init_module_, pair_block_inputs
 
-    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
-    cores = min(cores, 16)
-    torch.set_num_threads(cores)
+    cfg = CONFIGS[cfg_name]
     bf16 = cfg["dtype"] == "bf16"
-    n_full = cfg["n"] if cfg["kind"] != "diffusion" else 384
-    for n in (n_full, 256, 128):
-        if n > 384:
+    autocast = lambda: torch.amp.autocast("cpu", dtype=torch.bfloat16, enabled=bf16)  # noqa: E731
+    if leg == "cpp":
+        from oracle import cpp_port
+        cpp_port.load()
+    if cfg["kind"] == "diffusion":
+        m = init_module_(R.DiffusionTransformer().eval(), seed=0)
+        inp = diffusion_inputs(cfg["n"], samples=cfg["samples"])
+        act = inp.act.bfloat16().float() if bf16 else inp.act
+        run_module = m if leg == "torch" else cpp_port.DiffusionTransformerCpp(m)
+
+        def fn():
+            with torch.inference_mode(), autocast():
+                for s in range(cfg["samples"]):
+                    run_module(act[s].clone(), inp.mask, inp.single_cond, inp.pair_cond)
+        return fn, f"24-block diffusion transformer, {cfg['samples']} samples, N={cfg['n']}", 1, 1
+    with_single = cfg["with_single"]
+    block = init_module_(R.PairformerBlock(with_single=with_single).eval(), seed=0)
+    inp = pair_block_inputs(cfg["n"], pad=cfg["pad"], random_pad=cfg["random_pad"], seed=0, with_single=with_single)
+    pair = inp.pair.bfloat16() if bf16 else inp.pair
+    single = (inp.single.bfloat16() if bf16 else inp.single) if with_single else None
+    chunked = lambda *a, **k: R.dot_product_attention_chunked(*a, rows_per_chunk=32, **k)  # noqa: E731
+    run_block = block if leg == "torch" else cpp_port.PairformerBlockCpp(block)
+
+    def fn():
+        with torch.inference_mode(), autocast():
+            if with_single:
+                run_block(pair.clone(), inp.pair_mask, single.clone(), inp.seq_mask, attention=chunked)
+            else:
+                run_block(pair.clone(), inp.pair_mask, attention=chunked)
+    blocks = cfg.get("blocks", 1)
+    what = (f"one Pairformer block at N={cfg['n']}{' with single track' if with_single else ' (pair stack)'}, "
+            f"{'bf16 CPU autocast' if bf16 else 'fp32'}")
+    return fn, what, 1, blocks
+
+
+def cpu_baseline(cfg_name, runs=3):
+    """The reference's CPU backends restated and timed on this host (BASELINE.md protocol):
+    1 warm-up then the median of ``runs`` runs, on ``cpu_threads()`` threads. The torch leg is
+    oracle.restatement (the reference's torch backend); the cpp leg is oracle.cpp_port (the
+    af3_kernels algorithms). ``value`` is the torch leg, in ms per Pairformer block (per
+    transformer forward for C4); C3's 48-block figure is one block's time x 48."""
+    import torch
+    threads = cpu_threads()
+    torch.set_num_threads(threads)
+    legs = {}
+    for leg in ("torch", "cpp"):
+        try:
+            fn, what, per_call, factor = cpu_workload(cfg_name, leg)
+        except (ImportError, RuntimeError, OSError) as err:
+            legs[leg] = {"status": f"unavailable: {err}"}
             continue
-        block = init_module_(R.PairformerBlock(with_single=False).eval(), seed=0)
-        inp = pair_block_inputs(n, pad=max(1, n // 12), seed=0, with_single=False)
-        pair = inp.pair.bfloat16() if bf16 else inp.pair
-        attention = R.dot_product_attention_chunked
-        t0 = time.perf_counter()
-        with torch.inference_mode(), torch.amp.autocast("cpu", dtype=torch.bfloat16, enabled=bf16):
-            block(pair.clone(), inp.pair_mask, attention=lambda *a, **k: attention(*a, rows_per_chunk=32, **k))
-        dt = time.perf_counter() - t0
-        if dt <= budget_s or n == 128:
-            return {"value": round(dt * 1e3, 1), "unit": "ms per Pairformer pair block", "cores": cores,
-                    "kind": "port",
-                    "sample": f"1 pair block (TriMul out/in, TriAtt start/end, Transition) at N={n}, "
-                              f"{'bf16 CPU autocast' if bf16 else 'fp32'}, torch CPU restatement "
-                              f"of the reference torch backend, {cores} threads"}
-    return None
+        median, times = _median_ms(fn, runs=runs)
+        rec = {"ms_per_block" if cfg_name != "C4" else "ms_per_forward": round(median / per_call, 1),
+               "runs_ms": times, "sample": what}
+        if factor > 1:
+            rec["ms_per_trunk_extrapolated"] = round(median / per_call * factor, 1)
+            rec["extrapolation"] = f"one block x {factor}"
+        legs[leg] = rec
+        log(f"cpu {leg}: {rec}")
+    torch_leg = legs.get("torch", {})
+    value = torch_leg.get("ms_per_block", torch_leg.get("ms_per_forward"))
+    return {"value": value, "unit": "ms per Pairformer block" if cfg_name != "C4" else "ms per transformer forward",
+            "cores": threads, "kind": "port",
+            "sample": f"{torch_leg.get('sample', cfg_name)}; 1 warm-up + median of {runs}; "
+                      "restatements of the reference's torch and cpp (af3_kernels) backends",
+            "legs": legs, "host": host_cpu()}
+
+
+def run_config(cfg_name, steps, warmup, device, graph=False):
+    """Times ``steps`` steps of one configuration after ``warmup`` untimed ones (bracketed by
+    device synchronisation, HIP events on the launch stream), then the per-kernel rooflines
+    over a few more steps with the library's launch timers on."""
+    import torch
+    log(f"config {cfg_name}: building workload")
+    step, blocks, workload, cfg = build_workload(cfg_name, device)
+    for i in range(warmup):
+        step()
+        if i == 0 or i + 1 == warmup:
+            log(f"{cfg_name} warmup {i + 1}/{warmup}")
+    torch.cuda.synchronize()
+    run = step
+    if graph:
+        # The step records no memset, host copy or synchronisation, so it replays as a graph.
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step()
+        torch.cuda.synchronize()
+        run = g.replay
+        log("captured one step in a HIP graph")
+    stream = torch.cuda.current_stream(device)
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        run()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_step = start.elapsed_time(stop) / steps
+    log(f"{cfg_name} timed {steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
+    roof, kernels = None, None
+    if cfg["kind"] != "diffusion":
+        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(steps, 5)))
+        log(f"{cfg_name} roofline: {roof}")
+    return dict(ms_step=ms_step, blocks=blocks, workload=workload, cfg=cfg, roofline=roof, kernels=kernels)
 
 
 def main():
@@ -217,43 +366,26 @@ def main():
         raise SystemExit("bench.py needs a ROCm device")
     native_hip.load_library()
     device = torch.device("cuda:0")
-    log(f"config {args.config}: building workload")
-    step, blocks, workload, cfg = build_workload(args.config, device)
-    for i in range(args.warmup):
-        step()
-        if i == 0 or i + 1 == args.warmup:
-            log(f"warmup {i + 1}/{args.warmup}")
-    torch.cuda.synchronize()
-    run = step
-    if args.graph:
-        # The step records no memset, host copy or synchronisation, so it replays as a graph.
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            step()
-        torch.cuda.synchronize()
-        run = graph.replay
-        log("captured one step in a HIP graph")
-    stream = torch.cuda.current_stream(device)
-    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t0 = time.perf_counter()
-    start.record(stream)
-    for _ in range(args.steps):
-        run()
-    stop.record(stream)
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    ms_step = start.elapsed_time(stop) / args.steps
-    log(f"timed {args.steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
+    res = run_config(args.config, args.steps, args.warmup, device, graph=args.graph)
+    ms_step, blocks, cfg = res["ms_step"], res["blocks"], res["cfg"]
     value = ms_step / blocks
 
-    roof, kernels = None, None
-    if cfg["kind"] != "diffusion":
-        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(args.steps, 5)))
-        log(f"roofline: {roof}")
+    # The north-star target (C3, the 48-block trunk at N=768) is timed beside the metric's
+    # N=384 configuration in the default run.
+    c3 = None
+    if args.config == "C2" and not args.no_c3:
+        c3_steps, c3_warmup = DEFAULT_STEPS["C3"]
+        r3 = run_config("C3", c3_steps, c3_warmup, device, graph=args.graph)
+        c3 = {"ms_per_block": round(r3["ms_step"] / r3["blocks"], 4), "ms_per_trunk": round(r3["ms_step"], 3),
+              "steps": c3_steps, "warmup": c3_warmup, "config": r3["workload"], "roofline": r3["roofline"],
+              "kernels": r3["kernels"]}
+
     base = None
     if not args.no_cpu_baseline:
-        log("cpu baseline (oracle on host cores)")
-        base = cpu_baseline(cfg)
+        log("cpu baseline (restatements on host cores)")
+        base = cpu_baseline(args.config)
+        if c3 is not None:
+            c3["cpu_baseline"] = cpu_baseline("C3")
         log(f"cpu baseline: {base}")
 
     if args.copy_calibration_mb:
@@ -271,8 +403,8 @@ def main():
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,1/fan_in) weights)",
-        "config": dict(workload, launch="hip graph replay" if args.graph else "eager"),
-        "roofline": roof, "cpu_baseline": base, "kernels": kernels,
+        "config": dict(res["workload"], launch="hip graph replay" if args.graph else "eager"),
+        "roofline": res["roofline"], "cpu_baseline": base, "kernels": res["kernels"], "c3": c3,
     }
     print(json.dumps(line), flush=True)
 

@@ -1,9 +1,14 @@
-"""The error floor of bf16-operand matrix arithmetic (test infrastructure only).
+"""The error floor of bf16 matrix arithmetic (test infrastructure only).
 
 Each function re-evaluates a reference operator in float64 with ONLY the operands of its
 matrix products rounded to bf16 (activations and weights entering a matmul, attention
-probabilities and values), accumulating in float64 and keeping every other step exact.
-No implementation that feeds bf16 operands to matrix cores can be systematically more
+probabilities and values), plus the two intermediates that the reference's own bf16
+backends hold in bf16 between their GEMMs: the triangle-multiplication contraction
+(``af3_kernels/src/csrc/triangle_multiplication.cpp:61-63``, a ``tiled_matmul`` result in
+the compute dtype; ``torch.einsum`` under autocast) and the attention output P.V
+(``af3_kernels/src/csrc/dot_product_attention.cpp:99-102``, a GEMM into the output dtype).
+Accumulation is float64 and every other step exact. No implementation that feeds bf16
+operands to matrix cores and keeps those two tensors in bf16 can be systematically more
 accurate; the distance of this result from the exact (float64) operator is the floor
 against which the HIP bf16 path is judged.
 
@@ -42,7 +47,7 @@ def triangle_multiplication(m, pair, mask):
         p = p * mask.double()[None]
     p = p * torch.sigmoid(_lin(x, m.gate.weight).permute(2, 0, 1))
     p = p.reshape(m.c_pair, 2, *p.shape[1:])
-    out = torch.einsum(m.equation, _r(p[:, 0]), _r(p[:, 1])).permute(1, 2, 0)
+    out = _r(torch.einsum(m.equation, _r(p[:, 0]), _r(p[:, 1]))).permute(1, 2, 0)
     out = _lin(_ln(out, m.center_norm), m.output_projection.weight)
     return out * torch.sigmoid(_lin(x, m.gating_linear.weight))
 
@@ -56,7 +61,7 @@ def grid_self_attention(m, pair, mask):
                for n in ("q_projection", "k_projection", "v_projection"))
     logits = _r(q * q.shape[-1] ** -0.5) @ _r(k).transpose(-1, -2) + bias
     logits = logits.masked_fill(~mask.bool()[:, None, None, :], -1e9)
-    o = R._heads_last(_r(torch.softmax(logits, -1)) @ _r(v))
+    o = R._heads_last(_r(_r(torch.softmax(logits, -1)) @ _r(v)))
     o = _lin(o * torch.sigmoid(_lin(x, m.gating_query.weight)), m.output_projection.weight)
     return o.permute(1, 0, 2) if m.transpose else o
 
@@ -86,6 +91,14 @@ def _round_operand(t):
     return t
 
 
+def _to_float64(t):
+    if isinstance(t, torch.Tensor) and t.dtype == torch.float32:
+        return t.to(torch.float64)
+    if isinstance(t, (list, tuple)):
+        return type(t)(_to_float64(x) for x in t)
+    return t
+
+
 def mark_residual(t: torch.Tensor) -> torch.Tensor:
     """Marks ``t`` as a bf16 residual stream for :class:`Bf16Operands`: every in-place
     update ``t += update`` under the mode is rounded to bf16, as an update of a bf16 pair,
@@ -99,27 +112,45 @@ class Bf16Operands(TorchFunctionMode):
     """While active, every matrix product of the restatement (``nn.Linear``'s
     ``F.linear``, ``torch.matmul``/``@``, ``torch.einsum``, ``bmm``/``mm``) sees its
     operands rounded to bf16 and keeps its accumulation in the caller's dtype (fp32 or
-    float64); LayerNorm, softmax, sigmoid, the mask fill and the residual adds stay
-    exact, except that an in-place add into a tensor marked by :func:`mark_residual` is
-    rounded to bf16 afterwards. Running ``oracle.restatement``'s modules under this mode
+    float64); the contraction (the restatement's only ``einsum``) and the attention output
+    (a product whose left operand is a softmax) are rounded to bf16 as well; LayerNorm,
+    softmax, sigmoid, the mask fill and the residual adds stay exact, except that an
+    in-place add into a tensor marked by :func:`mark_residual` is rounded to bf16
+    afterwards. Running ``oracle.restatement``'s modules under this mode
     gives the bf16 floor of any composition of them (a whole PairformerBlock, the 24-block
     DiffusionTransformer) in the same sense as the per-operator functions above, which it
     reproduces (tests/test_oracle.py)."""
 
+    def __init__(self, float64: bool = False):
+        super().__init__()
+        self.float64 = float64
+
     def __torch_function__(self, func, types, args=(), kwargs=None):
         kwargs = kwargs or {}
         name = getattr(func, "__name__", "")
+        if self.float64 and not name.endswith("_"):
+            # Every out-of-place op evaluates in float64 (fp32 parameters and inputs are
+            # exact in it): the same floor with another accumulation precision, hence
+            # another realization of its rounding pattern.
+            args, kwargs = _to_float64(args), {k: _to_float64(v) for k, v in kwargs.items()}
         if name in ("add_", "__iadd__") and getattr(args[0], "_bf16_residual", False):
             out = func(*args, **kwargs)
             out.copy_(out.to(torch.bfloat16))
             return out
-        if name in _PRODUCTS:
-            if name == "linear":
-                args = tuple(_round_operand(a) if i < 2 else a for i, a in enumerate(args))
-                if "weight" in kwargs:
-                    kwargs = dict(kwargs, weight=_round_operand(kwargs["weight"]))
-            elif name == "einsum":
-                args = (args[0],) + tuple(_round_operand(a) for a in args[1:])
-            else:
-                args = tuple(_round_operand(a) for a in args)
-        return func(*args, **kwargs)
+        if name == "softmax":
+            out = func(*args, **kwargs)
+            out._softmax_output = True
+            return out
+        if name not in _PRODUCTS:
+            return func(*args, **kwargs)
+        stored = name == "einsum" or getattr(args[0], "_softmax_output", False)
+        if name == "linear":
+            args = tuple(_round_operand(a) if i < 2 else a for i, a in enumerate(args))
+            if "weight" in kwargs:
+                kwargs = dict(kwargs, weight=_round_operand(kwargs["weight"]))
+        elif name == "einsum":
+            args = (args[0],) + tuple(_round_operand(a) for a in args[1:])
+        else:
+            args = tuple(_round_operand(a) for a in args)
+        out = func(*args, **kwargs)
+        return _round_operand(out) if stored else out

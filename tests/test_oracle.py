@@ -265,8 +265,9 @@ def test_bf16_operand_floor_exceeds_the_max_abs_form_of_the_bf16_bar():
 
 def test_bf16_operand_mode_rounds_only_product_operands():
     """Bf16Operands rounds the operands of F.linear (not its bias), matmul, @ and einsum,
-    and leaves every other op exact: a planted product on unrounded operands, or a
-    rounded bias, would differ."""
+    the outputs of einsum (the contraction) and of a product whose left operand is a
+    softmax (the attention output), and leaves every other op exact: a planted product on
+    unrounded operands, a rounded bias or a rounded logit product would differ."""
     from oracle.bf16_floor import Bf16Operands
     g = torch.Generator().manual_seed(1)
     x, w, b = (torch.randn(5, 7, generator=g, dtype=torch.float64),
@@ -278,11 +279,15 @@ def test_bf16_operand_mode_rounds_only_product_operands():
         mm, at = torch.matmul(x, w.T), x @ w.T
         es = torch.einsum("ik,jk->ij", x, w)
         sm = torch.softmax(x, -1)
+        pv = torch.matmul(sm, w.T)
     assert torch.equal(lin, r(x) @ r(w).T + b)
     assert not torch.equal(lin, r(x) @ r(w).T + r(b))
-    for t in (mm, at, es):
+    for t in (mm, at):
         assert torch.equal(t, r(x) @ r(w).T)
+        assert not torch.equal(t, r(r(x) @ r(w).T))
+    assert torch.equal(es, r(r(x) @ r(w).T))
     assert torch.equal(sm, torch.softmax(x, -1))
+    assert torch.equal(pv, r(r(torch.softmax(x, -1)) @ r(w).T))
 
 
 @pytest.mark.parametrize("transpose", [False, True])
