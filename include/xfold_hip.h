@@ -175,6 +175,25 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
                                 void *out, int out_dtype, int accumulate,
                                 void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Scratch bytes of xfh_triangle_multiplication_noalloc on each device (128 MiB: the bf16
+ * c = 128 path up to n = 418, the fp32 path up to n = 161). */
+#define XFH_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
+
+/* xfh_triangle_multiplication without a workspace argument: the same arguments, result and
+ * kernels, with the scratch in a device array the library holds on each device (of
+ * XFH_NOALLOC_SCRATCH_BYTES; larger problems fail with XFH_EUNSUPPORTED). Allocates
+ * nothing, so callers that cannot allocate device memory can use it: code under HIP graph
+ * capture, serving loops and harnesses that forbid hipMalloc. Calls on one device share
+ * the scratch, so calls that overlap on one device (other streams, other host threads)
+ * race; calls ordered on one stream do not. No counterpart in the reference. */
+int xfh_triangle_multiplication_noalloc(const void *pair, int pair_dtype, const void *mask, int mask_dtype,
+                                        int64_t n, int64_t c, int outgoing,
+                                        const float *left_w, const float *left_b, float left_eps,
+                                        const void *proj_w, const void *gate_w,
+                                        const float *center_w, const float *center_b, float center_eps,
+                                        const void *out_w, const void *gating_w, int dtype,
+                                        void *out, int out_dtype, int accumulate, void *stream);
+
 /* Grid (triangle) self-attention over a contiguous [n, n, c] pair tensor: starting node
  * (transpose = 0) or ending node (transpose = 1). Same output/accumulate contract as
  * xfh_triangle_multiplication. Replaces GridSelfAttention.forward

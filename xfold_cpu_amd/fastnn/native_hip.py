@@ -59,6 +59,8 @@ SIGNATURES = {
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
     "xfh_triangle_multiplication": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,
                                          _f, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
+    "xfh_triangle_multiplication_noalloc": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,
+                                                 _f, _p, _p, _i, _p, _i, _i, _p]),
     "xfh_grid_self_attention_workspace_size": (_i64, [_i64, _i64, _i64, _i]),
     "xfh_grid_self_attention": (_i, [_p, _i, _p, _i, _i64, _i64, _i64, _i, _p, _p, _f, _p, _p, _p,
                                      _p, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
