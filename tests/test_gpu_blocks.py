@@ -217,3 +217,71 @@ def test_unpacked_bias_beyond_the_attention_key_limit(device, monkeypatch):
         with autocast(True):
             got = hip(act.to(device).clone(), mask.to(device), scond.to(device), pcond.to(device))
     assert_parity_bf16(got, want, "diffusion transformer (limit 32)", floor=floor_of(lambda: oracle(residual)))
+
+
+def test_diffusion_input_cache_skips_the_pair_logits_on_repeat_calls(device):
+    """Inside an input-cache scope (the reference's InputCache rules) a second call with the
+    same pair_cond, single_cond and weights reuses the packed pair logits and the block
+    conditioning (no pair_bias_kernel launch) and gives the same result bit for bit; an
+    in-place update of pair_cond invalidates them."""
+    from xfold_cpu_amd.fastnn import config
+    from xfold_cpu_amd.fastnn import native_hip as nh
+    from xfold_cpu_amd.nn.cache import input_cache_scope
+    args = dict(c_act=256, c_single_cond=64, c_pair_cond=128, num_head=16, num_blocks=4, super_block_size=2)
+    _, hip = pair_of("DiffusionTransformer", args, seed=8, device=device)
+    g = torch.Generator().manual_seed(8)
+    n = 50
+    act = torch.randn(3, n, 256, generator=g).bfloat16().to(device)
+    mask = torch.ones(n, device=device)
+    scond, pcond = torch.randn(n, 64, generator=g).to(device), torch.randn(n, n, 128, generator=g).to(device)
+
+    def run():
+        nh.kernel_timing_read("pair_bias")
+        nh.set_kernel_timing(True)
+        try:
+            with torch.inference_mode(), autocast(True):
+                out = hip(act.clone(), mask, scond, pcond)
+            torch.cuda.synchronize()
+        finally:
+            nh.set_kernel_timing(False)
+        return out, nh.kernel_timing_read("pair_bias")[1]
+    saved = config.input_cache_enabled
+    config.input_cache_enabled = True
+    try:
+        with torch.no_grad(), input_cache_scope():
+            first, launches1 = run()
+            second, launches2 = run()
+            pcond.add_(0.5)
+            third, launches3 = run()
+        uncached, launches4 = run()                     # outside the scope: recomputed
+    finally:
+        config.input_cache_enabled = saved
+    assert (launches1, launches2, launches3, launches4) == (1, 0, 1, 1)
+    assert torch.equal(first, second)
+    assert torch.equal(third, uncached)
+    assert not torch.equal(first, third)
+
+
+def test_glu_reuses_its_packed_weight_with_a_foreign_cache(device):
+    """gated_linear_unit(x, weight, weight_cache) with a cache object of the reference's
+    kind (not a HipWeightCache) packs the weight once per weight version."""
+    import importlib
+    from xfold_cpu_amd import fastnn
+    glu_mod = importlib.import_module("xfold_cpu_amd.fastnn.gated_linear_unit")
+
+    class GLUWeightCache:                 # a stand-in with the reference's name and no methods used
+        pass
+    cache = GLUWeightCache()
+    lin = torch.nn.Linear(128, 2 * 256, bias=False).to(device)
+    x = torch.randn(40, 128, device=device)
+    with torch.inference_mode(), autocast(True):
+        a = fastnn.gated_linear_unit(x, lin.weight.T, weight_cache=cache)
+        packed = glu_mod._attached[cache]._value
+        b = fastnn.gated_linear_unit(x, lin.weight.T, weight_cache=cache)
+        assert glu_mod._attached[cache]._value is packed
+    assert torch.equal(a, b)
+    with torch.no_grad():
+        lin.weight.mul_(2)
+    with torch.inference_mode(), autocast(True):
+        fastnn.gated_linear_unit(x, lin.weight.T, weight_cache=cache)
+        assert glu_mod._attached[cache]._value is not packed

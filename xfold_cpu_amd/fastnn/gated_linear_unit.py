@@ -4,11 +4,30 @@
 
 from __future__ import annotations
 
+import weakref
+
 import torch
 
 from . import config as fastnn_config
 from . import native_hip as nh
 from . import ops
+
+# Device caches attached to caller-owned cache objects that are not HipWeightCaches (the
+# reference's GLUWeightCache, xfold/fastnn/gated_linear_unit.py:6-48, which Transition
+# passes on every call): one packed copy per such object, released with it.
+_attached = weakref.WeakKeyDictionary()
+
+
+def _device_cache(weight_cache):
+    if weight_cache is None or isinstance(weight_cache, nh.HipWeightCache):
+        return weight_cache
+    try:
+        cache = _attached.get(weight_cache)
+        if cache is None:
+            cache = _attached[weight_cache] = nh.HipWeightCache()
+        return cache
+    except TypeError:                 # not weak-referenceable: no reuse across calls
+        return None
 
 
 def gated_linear_unit_hip(x: torch.Tensor, weight: torch.Tensor, weight_cache=None) -> torch.Tensor:
@@ -17,8 +36,9 @@ def gated_linear_unit_hip(x: torch.Tensor, weight: torch.Tensor, weight_cache=No
     if weight.dim() != 2 or weight.shape[1] % 2 or weight.shape[0] != x.shape[-1]:
         raise ValueError("gated_linear_unit: weight must be [K, 2F] matching x's last dim")
     f = weight.shape[1] // 2
-    # The cache holds the packed copy of weight.T ([2F, K], nn.Linear layout).
-    cache = weight_cache if isinstance(weight_cache, nh.HipWeightCache) else None
+    # The cache holds the packed copy of weight.T ([2F, K], nn.Linear layout), keyed on the
+    # weight's version like the reference's GLUWeightCache.
+    cache = _device_cache(weight_cache)
     source = weight.T
     packed = cache.get(source, dtype, "glu") if cache is not None else nh._prepare(source, dtype, "glu")
     return ops.gated_linear_unit(x, packed, f, dtype)

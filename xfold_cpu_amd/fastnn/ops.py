@@ -211,10 +211,12 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
             mask = mask[None, None, None, :]
         elif mask.dim() == 2:
             mask = mask[:, None, None, :]
-        if mask.dtype not in (torch.bool, torch.uint8):
-            mask = mask.to(torch.bool)          # the reference's .to(bool) (attention.py:57-61)
+        # The kernels read float masks as the reference's .to(bool) does (nonzero, NaN
+        # included, keeps the key: attention.py:57-61), so no conversion is launched.
+        if mask.dtype not in (torch.bool, torch.uint8, torch.float32, torch.bfloat16):
+            mask = mask.to(torch.bool)
         mask_t = mask.expand(B, H, Q, K)
-        mask_code = nh.BOOL
+        mask_code = nh.BOOL if mask.dtype in (torch.bool, torch.uint8) else nh.dtype_code(mask.dtype)
         mask_strides = tuple(mask_t.stride())
     bias_t, bias_code, bias_strides = None, nh.F32, (0, 0, 0, 0)
     if isinstance(bias, PackedBias):

@@ -20,6 +20,7 @@ from ..fastnn import LayerNorm
 from ..fastnn import config as fastnn_config
 from ..fastnn import native_hip as nh
 from ..fastnn import ops
+from .cache import InputCache
 
 
 def _adaptive_layer_norm(aln: nn.Module, x: torch.Tensor, single_cond: Optional[torch.Tensor],
@@ -211,19 +212,35 @@ def _block_conditioning(module: nn.Module, single_cond: torch.Tensor, dtype: tor
             for i in range(n_blocks)]
 
 
+def _cached(module: nn.Module, name: str, dependencies, factory, modules):
+    """``module._input_cache.get`` (``xfold/nn/diffusion_transformer.py:255-265``) when the
+    module carries an input cache (this package's or the reference's InputCache, which share
+    the interface), else ``factory()``."""
+    cache = getattr(module, "_input_cache", None)
+    if cache is None:
+        return factory()
+    return cache.get(name, dependencies, module, factory, modules=modules)
+
+
 def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.Tensor,
                               single_cond: torch.Tensor, pair_cond: torch.Tensor) -> torch.Tensor:
     """``DiffusionTransformer.forward`` (``diffusion_transformer.py:250-272``), updating
-    ``act`` ([N, c] or [S, N, c], contiguous) in place and returning it."""
+    ``act`` ([N, c] or [S, N, c], contiguous) in place and returning it.
+
+    Inside an input-cache scope (``xfold_cpu_amd.nn.cache``, the reference's ``InputCache``
+    rules) the packed pair logits of every super-block and every block's conditioning are
+    kept across calls with the same ``pair_cond`` / ``single_cond`` and weights, as the
+    reference keeps its pair logits (``:255-265``)."""
     nh.check_gpu_inference(act, mask, single_cond, pair_cond)
     if not act.is_contiguous():
         raise ValueError("DiffusionTransformer (hip) updates act in place; pass a contiguous tensor")
     dtype = nh.compute_dtype(act, module.pair_logits_projection[0].weight)
     ln = module.pair_input_layer_norm
     heads, size = module.num_head, module.super_block_size
-    conds = _block_conditioning(module, single_cond, dtype, act.dtype)
-    if mask is not None and mask.dtype not in (torch.bool, torch.uint8):
-        mask = mask.to(torch.bool)      # once, not per block (xfold/fastnn/attention.py:57-61)
+    blocks = list(module.self_attention) + list(module.transition_block)
+    conds = _cached(module, "block_conditioning", (single_cond,),
+                    lambda: _block_conditioning(module, single_cond, dtype, act.dtype),
+                    modules=[b.adaptive_layernorm for b in blocks] + [b.adaptive_zero_init for b in blocks])
     n_blocks = module.num_super_blocks * size
     # A packed bias (either path below) feeds the pipelined attention kernel, which takes
     # bf16, head dims <= 64 and at most attention_max_keys() keys.
@@ -236,7 +253,9 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         projs = [module.pair_logits_projection[s].weight for s in range(module.num_super_blocks)]
         w_all = nh.derived_weight(module, f"pair_logits:{dtype}", projs,
                                   lambda *ws: torch.cat([w.detach() for w in ws], dim=0).to(dtype).contiguous())
-        packed = ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln)
+        packed = _cached(module, "pair_logits_packed", (pair_cond, heads),
+                         lambda: ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln),
+                         modules=(ln, module.pair_logits_projection))
         for index in range(n_blocks):
             att_cond, tr_cond = (None, None) if conds is None else conds[index]
             bias = ops.PackedBias(packed[index * heads:(index + 1) * heads])
@@ -372,6 +391,7 @@ class DiffusionTransformer(nn.Module):
             [SelfAttention(c_act, c_single_cond, use_single_cond=True) for _ in range(num_blocks)])
         self.transition_block = nn.ModuleList(
             [DiffusionTransition(c_act, c_single_cond, use_single_cond=True) for _ in range(num_blocks)])
+        self._input_cache = InputCache()
 
     def forward(self, act, mask, single_cond, pair_cond):
         _require(fastnn_config.dot_product_attention_implementation, "dot_product_attention_implementation")
