@@ -100,3 +100,73 @@ def triangle_multiplication(pair, mask, params, outgoing):
             gate = linear(normed[i][j], params["gating"])
             out[i][j] = [projected[o] * _sigmoid(gate[o]) for o in range(c)]
     return out
+
+
+def outer_product_mean(msa, mask, params, eps=1e-3):
+    """OuterProductMean (``xfold/nn/primitives.py:40-72``) by loops: per row (s, i), LN then
+    left/right = mask[s][i] * (W x); out[i][j][f] = (sum over c, e of (sum over s of
+    left[s][i][c] right[s][j][e]) w[c][e][f] + b[f]) / (eps + sum over s of mask[s][i]
+    mask[s][j]). msa: [S][N][C]; params: ln_w, ln_b, left [c][C], right [c][C],
+    w [c][c][F], b [F]."""
+    rows, n = len(msa), len(msa[0])
+    cc = len(params["left"])
+
+    def linear(x, w):
+        return [sum(w[o][t] * x[t] for t in range(len(x))) for o in range(len(w))]
+
+    left = [[None] * n for _ in range(rows)]
+    right = [[None] * n for _ in range(rows)]
+    for s in range(rows):
+        for i in range(n):
+            x = layer_norm([msa[s][i]], params["ln_w"], params["ln_b"])[0]
+            left[s][i] = [mask[s][i] * v for v in linear(x, params["left"])]
+            right[s][i] = [mask[s][i] * v for v in linear(x, params["right"])]
+    f_out = len(params["b"])
+    out = [[None] * n for _ in range(n)]
+    for i in range(n):
+        for j in range(n):
+            norm = sum(mask[s][i] * mask[s][j] for s in range(rows))
+            vec = []
+            for f in range(f_out):
+                acc = params["b"][f]
+                for c in range(cc):
+                    for e in range(cc):
+                        outer = sum(left[s][i][c] * right[s][j][e] for s in range(rows))
+                        acc += outer * params["w"][c][e][f]
+                vec.append(acc / (eps + norm))
+            out[i][j] = vec
+    return out
+
+
+def msa_attention(msa, mask, pair, params, heads):
+    """MSAAttention (``xfold/nn/attention.py:108-144``) by loops: weights[h][q][k] =
+    softmax over k of (W_pair LN(pair[q][k]))[h] + 1e9 (max over s of mask[s][k] - 1);
+    out[s][q] = W_out((sum over k of weights[h][q][k] v[s][k][h, :]) * sigmoid(W_gate x))
+    with x = LN(msa[s][q]) and v = W_v x. msa: [S][N][C]; pair: [N][N][P]."""
+    rows, n, c = len(msa), len(msa[0]), len(msa[0][0])
+    dv = c // heads
+
+    def linear(x, w):
+        return [sum(w[o][t] * x[t] for t in range(len(x))) for o in range(len(w))]
+
+    key_bias = [1e9 * (max(mask[s][k] for s in range(rows)) - 1.0) for k in range(n)]
+    weights = [[None] * n for _ in range(heads)]
+    for q in range(n):
+        logits = [linear(layer_norm([pair[q][k]], params["pair_ln_w"], params["pair_ln_b"])[0], params["logits"])
+                  for k in range(n)]
+        for h in range(heads):
+            row = [logits[k][h] + key_bias[k] for k in range(n)]
+            top = max(row)
+            ex = [math.exp(x - top) for x in row]
+            total = sum(ex)
+            weights[h][q] = [e / total for e in ex]
+    out = [[None] * n for _ in range(rows)]
+    for s in range(rows):
+        xs = [layer_norm([msa[s][k]], params["ln_w"], params["ln_b"])[0] for k in range(n)]
+        vs = [linear(xs[k], params["v"]) for k in range(n)]
+        for q in range(n):
+            avg = [sum(weights[ch // dv][q][k] * vs[k][ch] for k in range(n)) for ch in range(c)]
+            gate = linear(xs[q], params["gate"])
+            gated = [avg[ch] * _sigmoid(gate[ch]) for ch in range(c)]
+            out[s][q] = linear(gated, params["out"])
+    return out

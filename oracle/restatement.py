@@ -251,6 +251,67 @@ class Transition(nn.Module):
         return self.transition2(gated_linear_unit(x, self.transition1.weight.T))
 
 
+class OuterProductMean(nn.Module):
+    """``xfold/nn/primitives.py:40-72``: LN(msa) -> masked left/right projections ->
+    out[i, j, f] = (sum_{c,e} (sum_s left[s,i,c] right[s,j,e]) output_w[c,e,f] + output_b[f])
+    / (1e-3 + sum_s mask[s,i] mask[s,j]). The reference's einsum pair ('acb,ade->dceb',
+    'dceb,cef->dbf', then permute(1, 0, 2)) is the same sum, indexed [j, ..., i] before the
+    final transpose."""
+
+    def __init__(self, c_msa: int = 64, num_output_channel: int = 128, num_outer_channel: int = 32) -> None:
+        super().__init__()
+        self.c_msa = c_msa
+        self.num_outer_channel = num_outer_channel
+        self.num_output_channel = num_output_channel
+        self.epsilon = 1e-3
+        self.layer_norm_input = LayerNorm(c_msa)
+        self.left_projection = nn.Linear(c_msa, num_outer_channel, bias=False)
+        self.right_projection = nn.Linear(c_msa, num_outer_channel, bias=False)
+        self.output_w = nn.Parameter(torch.randn(num_outer_channel, num_outer_channel, num_output_channel))
+        self.output_b = nn.Parameter(torch.randn(num_output_channel))
+
+    def forward(self, msa: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+        m = mask.unsqueeze(-1)                                    # [S, N, 1]
+        x = self.layer_norm_input(msa)
+        left = m * self.left_projection(x)                        # [S, N, c]
+        right = m * self.right_projection(x)
+        outer = torch.einsum("sic,sje->ijce", left, right)        # summed over sequences
+        act = torch.einsum("ijce,cef->ijf", outer, self.output_w) + self.output_b
+        norm = torch.einsum("si,sj->ij", mask, mask).unsqueeze(-1)
+        return act / (self.epsilon + norm)
+
+
+class MSAAttention(nn.Module):
+    """``xfold/nn/attention.py:108-144``: attention weights from the pair alone,
+    softmax(pair_logits(LN(pair)) + 1e9 (max_s msa_mask - 1)) over keys, shared by every
+    MSA row; each row averages its own values v = v_projection(LN(msa)) per head, gated by
+    sigmoid(gating_query(LN(msa))), then output_projection."""
+
+    def __init__(self, c_msa: int = 64, c_pair: int = 128, num_head: int = 8) -> None:
+        super().__init__()
+        self.c_msa = c_msa
+        self.c_pair = c_pair
+        self.num_head = num_head
+        self.value_dim = c_msa // num_head
+        self.act_norm = LayerNorm(c_msa)
+        self.pair_norm = LayerNorm(c_pair)
+        self.pair_logits = nn.Linear(c_pair, num_head, bias=False)
+        self.v_projection = nn.Linear(c_msa, num_head * self.value_dim, bias=False)
+        self.gating_query = nn.Linear(c_msa, c_msa, bias=False)
+        self.output_projection = nn.Linear(c_msa, c_msa, bias=False)
+
+    def forward(self, msa: torch.Tensor, msa_mask: torch.Tensor, pair: torch.Tensor) -> torch.Tensor:
+        x = self.act_norm(msa)
+        logits = self.pair_logits(self.pair_norm(pair)).permute(2, 0, 1)     # [H, q, k]
+        logits = logits + 1e9 * (msa_mask.max(dim=0).values - 1.0)            # masked keys
+        weights = torch.softmax(logits, dim=-1)
+        rows, n = x.shape[0], x.shape[1]
+        v = self.v_projection(x).reshape(rows, n, self.num_head, self.value_dim)
+        avg = torch.einsum("hqk,skhc->sqhc", weights, v).reshape(rows, n, self.c_msa)
+        avg = avg * torch.sigmoid(self.gating_query(x))
+        return self.output_projection(avg)
+
+
 class AdaptiveLayerNorm(nn.Module):
     """``xfold/nn/diffusion_transformer.py:27-64``.
 
@@ -407,6 +468,34 @@ class PairformerBlock(nn.Module):
         single += self.single_attention_(single, seq_mask, pair_logits=logits, attention=attn)
         single += self.single_transition(single)
         return pair, single
+
+
+class EvoformerBlock(nn.Module):
+    """``xfold/nn/pairformer.py:117-156``: pair += OuterProductMean(msa); msa +=
+    MSAAttention(msa, pair); msa += Transition(msa); then the five pair updates of the
+    Pairformer block (:149-154), each seeing the updated tensors."""
+
+    def __init__(self, c_msa: int = 64, c_pair: int = 128, n_heads_pair: int = 4) -> None:
+        super().__init__()
+        self.outer_product_mean = OuterProductMean(c_msa=c_msa, num_output_channel=c_pair)
+        self.msa_attention1 = MSAAttention(c_msa=c_msa, c_pair=c_pair)
+        self.msa_transition = Transition(c_msa)
+        self.triangle_multiplication_outgoing = TriangleMultiplication(c_pair, _outgoing=True)
+        self.triangle_multiplication_incoming = TriangleMultiplication(c_pair, _outgoing=False)
+        self.pair_attention1 = GridSelfAttention(c_pair, n_heads_pair, transpose=False)
+        self.pair_attention2 = GridSelfAttention(c_pair, n_heads_pair, transpose=True)
+        self.pair_transition = Transition(c_pair)
+
+    def forward(self, msa, pair, msa_mask, pair_mask, attention=None):
+        pair += self.outer_product_mean(msa, msa_mask)
+        msa += self.msa_attention1(msa, msa_mask, pair)
+        msa += self.msa_transition(msa)
+        pair += self.triangle_multiplication_outgoing(pair, mask=pair_mask)
+        pair += self.triangle_multiplication_incoming(pair, mask=pair_mask)
+        pair += self.pair_attention1(pair, mask=pair_mask, attention=attention)
+        pair += self.pair_attention2(pair, mask=pair_mask, attention=attention)
+        pair += self.pair_transition(pair)
+        return msa, pair
 
 
 class DiffusionTransformer(nn.Module):

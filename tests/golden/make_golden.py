@@ -9,7 +9,8 @@ with ``xfold_cpu_amd.synthetic.init_module_`` (LayerNorm affine jittered), runs 
 seeded inputs in fp32 and under CPU bf16 autocast, and saves inputs, the state_dict and
 outputs as ``.npz`` (data only). It covers the compositions that no closed form pins:
 grid self-attention (both nodes), Transition, SelfAttention with and without
-conditioning, DiffusionTransition, PairformerBlock and DiffusionTransformer.
+conditioning, DiffusionTransition, PairformerBlock, DiffusionTransformer and
+EvoformerBlock (with OuterProductMean and MSAAttention inside).
 """
 
 from __future__ import annotations
@@ -51,7 +52,7 @@ def main(reference: str):
     from xfold.fastnn import config
     from xfold.nn.attention import GridSelfAttention
     from xfold.nn.diffusion_transformer import DiffusionTransformer, DiffusionTransition, SelfAttention
-    from xfold.nn.pairformer import PairformerBlock
+    from xfold.nn.pairformer import EvoformerBlock, PairformerBlock
     from xfold.nn.primitives import Transition
 
     for flag in ("layer_norm_implementation", "dot_product_attention_implementation",
@@ -143,6 +144,24 @@ def main(reference: str):
     save("diffusion_transformer", mod, args,
          {"act": act0, "mask": dmask, "single_cond": scond, "pair_cond": pcond}, {"out": out},
          {"module": "DiffusionTransformer"})
+
+    # EvoformerBlock (OuterProductMean, MSAAttention and the MSA transition before the pair
+    # stack): the composition no closed form pins, with a partly masked MSA (a masked row,
+    # scattered masked entries, one column masked in every row).
+    n, s_rows = 6, 5
+    args = dict(c_msa=16, c_pair=32, n_heads_pair=4)
+    mod = init_module_(EvoformerBlock(**args).eval(), seed=8, ln_jitter=True)
+    msa0, pair0 = randn(s_rows, n, 16), randn(n, n, 32)
+    msa_mask = torch.from_numpy((rng.uniform(size=(s_rows, n)) > 0.25).astype(np.float32))
+    msa_mask[2] = 0.0
+    msa_mask[:, 4] = 0.0
+    seq = token_mask(n, 1)
+    pmask = seq[:, None] * seq[None, :]
+    with torch.inference_mode():
+        msa, pair = mod(msa0.clone(), pair0.clone(), msa_mask, pmask)
+    save("evoformer_block", mod, args,
+         {"msa": msa0, "pair": pair0, "msa_mask": msa_mask, "pair_mask": pmask},
+         {"msa": msa, "pair": pair}, {"module": "EvoformerBlock"})
 
 
 if __name__ == "__main__":

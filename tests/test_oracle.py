@@ -172,6 +172,7 @@ MODULES = {
     "DiffusionTransition": R.DiffusionTransition,
     "PairformerBlock": R.PairformerBlock,
     "DiffusionTransformer": R.DiffusionTransformer,
+    "EvoformerBlock": R.EvoformerBlock,
 }
 
 
@@ -194,6 +195,10 @@ def run_oracle_on_fixture(name):
             pair, single = module(inputs["pair"].clone(), inputs["pair_mask"], inputs["single"].clone(),
                                   inputs["seq_mask"])
             got = {"pair": pair, "single": single}
+        elif kind == "EvoformerBlock":
+            msa, pair = module(inputs["msa"].clone(), inputs["pair"].clone(), inputs["msa_mask"],
+                               inputs["pair_mask"])
+            got = {"msa": msa, "pair": pair}
         else:
             got = {"out": module(inputs["act"].clone(), inputs["mask"], inputs["single_cond"],
                                  inputs["pair_cond"])}
@@ -202,7 +207,8 @@ def run_oracle_on_fixture(name):
 
 @pytest.mark.parametrize("name", ["grid_attention_start", "grid_attention_end", "transition",
                                   "self_attention", "self_attention_cond", "diffusion_transition",
-                                  "pairformer_block", "pairformer_block_bf16", "diffusion_transformer"])
+                                  "pairformer_block", "pairformer_block_bf16", "diffusion_transformer",
+                                  "evoformer_block"])
 def test_oracle_reproduces_reference_golden_vectors(name):
     meta, got, want = run_oracle_on_fixture(name)
     tol = 1e-6 if not meta.get("autocast") else 1e-2
@@ -309,3 +315,67 @@ def test_grid_self_attention_rows_equal_full_rows(transpose):
         part = R.grid_self_attention_rows(module, pair, mask, rows)
     want = full.permute(1, 0, 2)[rows] if transpose else full[rows]
     assert rel_err(part, want) < 1e-6
+
+
+def _nested(t):
+    return t.detach().double().tolist()
+
+
+def test_outer_product_mean_matches_brute_force():
+    """OuterProductMean against plain loops over (s, i, j, c, e, f), with a masked row and a
+    masked entry, and the transposed output (a plausible index swap) ruled out."""
+    from xfold_cpu_amd.synthetic import init_module_
+    module = init_module_(R.OuterProductMean(c_msa=6, num_output_channel=5, num_outer_channel=3).eval(),
+                          seed=2, ln_jitter=True)
+    g = torch.Generator().manual_seed(2)
+    msa = torch.randn(4, 5, 6, generator=g, dtype=torch.float64)
+    mask = torch.ones(4, 5, dtype=torch.float64)
+    mask[1] = 0
+    mask[2, 3] = 0
+    module = module.double()
+    with torch.no_grad():
+        got = module(msa, mask)
+    params = dict(ln_w=_nested(module.layer_norm_input.weight), ln_b=_nested(module.layer_norm_input.bias),
+                  left=_nested(module.left_projection.weight), right=_nested(module.right_projection.weight),
+                  w=_nested(module.output_w), b=_nested(module.output_b))
+    want = torch.tensor(brute.outer_product_mean(_nested(msa), _nested(mask), params), dtype=torch.float64)
+    assert rel_err(got, want) < 1e-10
+    assert rel_err(got.transpose(0, 1), want) > 1e-2
+
+
+def test_msa_attention_matches_brute_force():
+    """MSAAttention against plain loops: pair-only weights shared by every MSA row, the key
+    mask from the maximum over rows (a column masked in every row gets weight 0), gating."""
+    from xfold_cpu_amd.synthetic import init_module_
+    module = init_module_(R.MSAAttention(c_msa=8, c_pair=6, num_head=2).eval(), seed=3, ln_jitter=True)
+    module = module.double()
+    g = torch.Generator().manual_seed(3)
+    msa = torch.randn(3, 5, 8, generator=g, dtype=torch.float64)
+    pair = torch.randn(5, 5, 6, generator=g, dtype=torch.float64)
+    mask = torch.ones(3, 5, dtype=torch.float64)
+    mask[:, 2] = 0                                     # key 2 masked in every row
+    mask[0, 4] = 0                                     # key 4 kept by the other rows
+    with torch.no_grad():
+        got = module(msa, mask, pair)
+    params = dict(ln_w=_nested(module.act_norm.weight), ln_b=_nested(module.act_norm.bias),
+                  pair_ln_w=_nested(module.pair_norm.weight), pair_ln_b=_nested(module.pair_norm.bias),
+                  logits=_nested(module.pair_logits.weight), v=_nested(module.v_projection.weight),
+                  gate=_nested(module.gating_query.weight), out=_nested(module.output_projection.weight))
+    want = torch.tensor(brute.msa_attention(_nested(msa), _nested(mask), _nested(pair), params, 2),
+                        dtype=torch.float64)
+    assert rel_err(got, want) < 1e-10
+
+
+def test_golden_catches_an_evoformer_order_mistake():
+    """The MSA attention must see the pair already updated by OuterProductMean
+    (xfold/nn/pairformer.py:146-147): the old pair fails the golden vector."""
+    meta, inputs, params, outputs = load_fixture("evoformer_block")
+    module = R.EvoformerBlock(**meta["args"]).eval()
+    module.load_state_dict(params)
+    with torch.inference_mode():
+        msa, pair = inputs["msa"].clone(), inputs["pair"].clone()
+        pair_before = pair.clone()
+        pair += module.outer_product_mean(msa, inputs["msa_mask"])
+        msa += module.msa_attention1(msa, inputs["msa_mask"], pair_before)
+        msa += module.msa_transition(msa)
+    assert rel_err(msa, outputs["msa"]) > 1e-4

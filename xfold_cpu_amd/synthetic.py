@@ -45,9 +45,14 @@ def init_module_(module: torch.nn.Module, seed: int = 0, ln_jitter: bool = False
                     value = np.ones(shape) if pname == "weight" else np.zeros(shape)
             elif tensor.dim() == 2:
                 value = rng.standard_normal(shape) / math.sqrt(shape[1])
+            elif tensor.dim() >= 3:
+                # OuterProductMean.output_w [c, e, f]: fan-in c * e
+                value = rng.standard_normal(shape) / math.sqrt(math.prod(shape[:-1]))
             else:
-                fan_in = owner.weight.shape[1]
-                value = rng.standard_normal(shape) / math.sqrt(fan_in)
+                w = getattr(owner, "weight", None)
+                if w is None:                       # OuterProductMean.output_b
+                    w = owner.output_w.reshape(-1, shape[0]).T
+                value = rng.standard_normal(shape) / math.sqrt(w.shape[1])
             tensor.copy_(torch.from_numpy(np.asarray(value, dtype=np.float32)))
     return module
 
