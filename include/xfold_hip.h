@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 6
+#define XFH_ABI_VERSION 7
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -217,6 +217,41 @@ int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t 
                    const void *w1_packed, const void *w2, int dtype,
                    void *out, int out_dtype, int accumulate,
                    void *workspace, int64_t workspace_bytes, void *stream);
+
+/* OuterProductMean of the Evoformer's MSA stack over a contiguous msa [rows, n, c_msa] with
+ * mask [rows, n] (NULL = all ones):
+ *   out[i, j, f] = (sum_{c,e} O[i, j, c, e] * w[f, c * c_outer + e] + b[f]) / (norm_eps + M[i, j])
+ *   O[i, j, c, e] = sum_s mask[s, i] L[s, i, c] * mask[s, j] R[s, j, e],
+ *   M[i, j] = sum_s mask[s, i] mask[s, j],  [L | R] = LN(msa) @ proj_w^T,
+ * proj_w [2 c_outer, c_msa] = [left_projection.weight; right_projection.weight], out_w
+ * [c_out, c_outer^2] = output_w permuted 'c e f -> f (c e)', out_b fp32 [c_out]. out is
+ * contiguous [n, n, c_out], stored or accumulated into (accumulate nonzero). c_outer a
+ * multiple of 4, at most 64; rows >= 1. Replaces OuterProductMean.forward
+ * (xfold/nn/primitives.py:40-72). */
+int64_t xfh_outer_product_mean_workspace_size(int64_t rows, int64_t n, int64_t c_msa, int64_t c_outer, int dtype);
+int xfh_outer_product_mean(const void *msa, int msa_dtype, const void *mask, int mask_dtype, int64_t rows,
+                           int64_t n, int64_t c_msa, int64_t c_outer, int64_t c_out, const float *ln_w,
+                           const float *ln_b, float ln_eps, const void *proj_w, const void *out_w,
+                           const float *out_b, float norm_eps, int dtype, void *out, int out_dtype,
+                           int accumulate, void *workspace, int64_t workspace_bytes, void *stream);
+
+/* MSA row attention with pair logits over msa [rows, n, c_msa], msa_mask [rows, n] (NULL =
+ * all ones) and pair [n, n, c_pair], all contiguous:
+ *   logits[h, q, k] = LN(pair)[q, k] . logits_w[h] + 1e9 * (max_s mask[s, k] - 1),
+ *   w = softmax over k (shared by every MSA row), v = LN(msa) @ v_w^T split into heads,
+ *   avg[s, q, h, :] = sum_k w[h, q, k] v[s, k, h, :],
+ *   out = (avg * sigmoid(LN(msa) @ gating_w^T)) @ out_w^T, stored or accumulated.
+ * logits_w [heads, c_pair], v_w/gating_w/out_w [c_msa, c_msa]; head dim c_msa / heads <= 16.
+ * With bf16 compute and c_pair = 128 the logits come from the pair-bias kernel of
+ * xfh_pair_attention_bias. Replaces MSAAttention.forward (xfold/nn/attention.py:108-144). */
+int64_t xfh_msa_attention_workspace_size(int64_t rows, int64_t n, int64_t c_msa, int64_t c_pair, int64_t heads,
+                                         int dtype);
+int xfh_msa_attention(const void *msa, int msa_dtype, const void *mask, int mask_dtype, const void *pair,
+                      int pair_dtype, int64_t rows, int64_t n, int64_t c_msa, int64_t c_pair, int64_t heads,
+                      const float *ln_w, const float *ln_b, float ln_eps, const float *pair_ln_w,
+                      const float *pair_ln_b, float pair_ln_eps, const void *logits_w, const void *v_w,
+                      const void *gating_w, const void *out_w, int dtype, void *out, int out_dtype, int accumulate,
+                      void *workspace, int64_t workspace_bytes, void *stream);
 
 #ifdef __cplusplus
 }

@@ -165,13 +165,15 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
       for (int e = 0; e < 4; ++e) {
         const int m = m0 + wm * 64 + i * 16 + row_lane + e;
         if (m >= p.M) continue;
-        TO *c = C + int64_t(m) * p.ldc + n;
+        TO *c = c_element(p, C, m, n);
         const TO *a = nullptr;
         if (aux) {
           const int64_t ar = p.aux_rows > 0 ? (m % p.aux_rows) : m;
           a = aux + batch * p.sAux + ar * p.ldaux + n;
         }
-        *c = from_f32<TO>(apply_epilogue<TO>(p.epi, acc[i][j][e] + bias, c, a));
+        float v = acc[i][j][e] + bias;
+        if (p.row_div) v /= p.row_div_eps + p.row_div[m];
+        *c = from_f32<TO>(apply_epilogue<TO>(p.epi, v, c, a));
       }
   }
 }

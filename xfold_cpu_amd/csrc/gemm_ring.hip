@@ -214,7 +214,7 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     for (int y = 0; y < 4; ++y) {
       const int m = m0 + wm * 64 + y * 16 + col;
       if (m >= p.M) continue;
-      TO *c = C + int64_t(m) * p.ldc + n;
+      TO *c = c_element(p, C, m, n);
       const TO *a = nullptr;
       if (aux) {
         const int64_t ar = p.aux_rows > 0 ? (m % p.aux_rows) : m;
@@ -233,8 +233,9 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
           if (a) av[e] = to_f32(a[e]);
         }
       }
+      const float rs = p.row_div ? 1.0f / (p.row_div_eps + p.row_div[m]) : 1.0f;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) out[e] = epilogue(p.epi, acc[x][y][e] + bias[e], cv[e], av[e]);
+      for (int e = 0; e < 4; ++e) out[e] = epilogue(p.epi, p.row_div ? (acc[x][y][e] + bias[e]) * rs : acc[x][y][e] + bias[e], cv[e], av[e]);
       if (full) {
         Vec4<TO>::store(c, out);
       } else {
@@ -307,6 +308,7 @@ RingPick pick_ring(const GemmArgs &p, int64_t batch, bool glu, int cus) {
 
 bool gemm_ring_supported(const GemmArgs &p, int out_dtype) {
   const int ob = out_dtype == XFH_BF16 ? 2 : 4;
+  if (p.pair_blk && (p.pair_blk % 4 || !aligned(p.C, 4 * ob) || p.sC % 4)) return false;
   const bool vec_out = p.ldc % 4 == 0 && p.sC % 4 == 0 && aligned(p.C, 4 * ob) &&
                        (!p.aux || (p.ldaux % 4 == 0 && p.sAux % 4 == 0 && aligned(p.aux, 4 * ob)));
   return p.K > 0 && p.K % 32 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sA % 8 == 0 &&

@@ -20,7 +20,22 @@ struct GemmArgs {
   int epi;                  // XFH_EPI_*
   int xcd_rows;             // gemm_ring: give each XCD a contiguous run of row-major tiles
   int glu_f;                // GLU output features (GLU launches only)
+  // Row divisor: the value (acc + bias) of row m is divided by (row_div_eps + row_div[m])
+  // before the epilogue (fp32 [M], null = none).
+  const float *row_div;
+  float row_div_eps;
+  // Pair-block output layout (0 = row-major): with blk > 0 the element (m, n) of an
+  // [M = I*blk] x [N = J*blk] product goes to C[((m/blk * J + n/blk) * blk + m%blk) * blk + n%blk],
+  // i.e. the [I][blk] x [J][blk] result stored as [I][J][blk][blk] (ldc unused).
+  int pair_blk;
 };
+
+// Address of element (m, n) of C (row-major, or the pair-block layout).
+template <typename TO> __device__ __forceinline__ TO *c_element(const GemmArgs &p, TO *C, int m, int n) {
+  if (p.pair_blk == 0) return C + int64_t(m) * p.ldc + n;
+  const int blk = p.pair_blk, jn = p.N / blk;
+  return C + ((int64_t(m / blk) * jn + n / blk) * blk + m % blk) * blk + n % blk;
+}
 
 int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s);
 // bf16-input GEMM with a direct-load LDS ring (gemm_ring.hip); gemm_nt routes to it when

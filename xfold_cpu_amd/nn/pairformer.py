@@ -1,5 +1,5 @@
-"""PairformerBlock with the reference's constructor, submodule names and call signature
-(``xfold/nn/pairformer.py:26-114``), running on the HIP backend.
+"""PairformerBlock and EvoformerBlock with the reference's constructors, submodule names and
+call signatures (``xfold/nn/pairformer.py:26-156``), running on the HIP backend.
 
 The block applies its five pair updates in place, each op's final kernel adding its
 result straight into ``pair`` (the residual ``pair += op(pair)`` of ``pairformer.py:96-100``
@@ -17,9 +17,9 @@ from ..fastnn import LayerNorm
 from ..fastnn import config as fastnn_config
 from ..fastnn import native_hip as nh
 from ..fastnn import ops
-from .attention import GridSelfAttention, grid_self_attention_hip
+from .attention import GridSelfAttention, MSAAttention, grid_self_attention_hip, msa_attention_hip
 from .diffusion_transformer import SelfAttention, self_attention_hip
-from .primitives import Transition, transition_hip
+from .primitives import OuterProductMean, Transition, outer_product_mean_hip, transition_hip
 from .triangle_multiplication import TriangleMultiplication, triangle_multiplication_hip
 
 
@@ -46,11 +46,7 @@ def pairformer_block_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.
     must be contiguous and are updated in place, as the reference's ``+=`` does."""
     if not pair.is_contiguous() or (single is not None and not single.is_contiguous()):
         raise ValueError("PairformerBlock (hip) updates pair/single in place; pass contiguous tensors")
-    triangle_multiplication_hip(block.triangle_multiplication_outgoing, pair, pair_mask, accumulate_into=pair)
-    triangle_multiplication_hip(block.triangle_multiplication_incoming, pair, pair_mask, accumulate_into=pair)
-    grid_self_attention_hip(block.pair_attention1, pair, pair_mask, accumulate_into=pair)
-    grid_self_attention_hip(block.pair_attention2, pair, pair_mask, accumulate_into=pair)
-    transition_hip(block.pair_transition, pair, accumulate_into=pair)
+    _pair_updates_hip(block, pair, pair_mask)
     if not block.with_single:
         return pair
     dtype = nh.compute_dtype(pair, block.single_pair_logits_projection.weight)
@@ -58,6 +54,22 @@ def pairformer_block_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.
     self_attention_hip(block.single_attention_, single, seq_mask, logits, None, accumulate_into=single)
     transition_hip(block.single_transition, single, accumulate_into=single)
     return pair, single
+
+
+def _pair_updates_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.Tensor) -> None:
+    triangle_multiplication_hip(block.triangle_multiplication_outgoing, pair, pair_mask, accumulate_into=pair)
+    triangle_multiplication_hip(block.triangle_multiplication_incoming, pair, pair_mask, accumulate_into=pair)
+    grid_self_attention_hip(block.pair_attention1, pair, pair_mask, accumulate_into=pair)
+    grid_self_attention_hip(block.pair_attention2, pair, pair_mask, accumulate_into=pair)
+    transition_hip(block.pair_transition, pair, accumulate_into=pair)
+
+
+def _require_hip_backends() -> None:
+    for name in ("layer_norm_implementation", "dot_product_attention_implementation",
+                 "gated_linear_unit_implementation", "triangle_multiplication_implementation"):
+        if getattr(fastnn_config, name) != fastnn_config.HIP:
+            raise ValueError(f"Unknown {name} for xfold_cpu_amd: "
+                             f"{getattr(fastnn_config, name)!r} (only 'hip')")
 
 
 class PairformerBlock(nn.Module):
@@ -81,9 +93,36 @@ class PairformerBlock(nn.Module):
             self.single_transition = Transition(c_x=c_single)
 
     def forward(self, pair, pair_mask, single=None, seq_mask=None):
-        for name in ("layer_norm_implementation", "dot_product_attention_implementation",
-                     "gated_linear_unit_implementation", "triangle_multiplication_implementation"):
-            if getattr(fastnn_config, name) != fastnn_config.HIP:
-                raise ValueError(f"Unknown {name} for xfold_cpu_amd: "
-                                 f"{getattr(fastnn_config, name)!r} (only 'hip')")
+        _require_hip_backends()
         return pairformer_block_hip(self, pair, pair_mask, single, seq_mask)
+
+
+def evoformer_block_hip(block: nn.Module, msa: torch.Tensor, pair: torch.Tensor, msa_mask: torch.Tensor,
+                        pair_mask: torch.Tensor):
+    """``EvoformerBlock.forward`` (``pairformer.py:139-156``): OuterProductMean into the pair,
+    MSA attention (over the updated pair) and transition into the MSA, then the five pair
+    updates. ``msa`` and ``pair`` must be contiguous and are updated in place."""
+    if not pair.is_contiguous() or not msa.is_contiguous():
+        raise ValueError("EvoformerBlock (hip) updates msa/pair in place; pass contiguous tensors")
+    outer_product_mean_hip(block.outer_product_mean, msa, msa_mask, accumulate_into=pair)
+    msa_attention_hip(block.msa_attention1, msa, msa_mask, pair, accumulate_into=msa)
+    transition_hip(block.msa_transition, msa, accumulate_into=msa)
+    _pair_updates_hip(block, pair, pair_mask)
+    return msa, pair
+
+
+class EvoformerBlock(nn.Module):
+    def __init__(self, c_msa: int = 64, c_pair: int = 128, n_heads_pair: int = 4) -> None:
+        super().__init__()
+        self.outer_product_mean = OuterProductMean(c_msa=c_msa, num_output_channel=c_pair)
+        self.msa_attention1 = MSAAttention(c_msa=c_msa, c_pair=c_pair)
+        self.msa_transition = Transition(c_x=c_msa)
+        self.triangle_multiplication_outgoing = TriangleMultiplication(c_pair=c_pair, _outgoing=True)
+        self.triangle_multiplication_incoming = TriangleMultiplication(c_pair=c_pair, _outgoing=False)
+        self.pair_attention1 = GridSelfAttention(c_pair=c_pair, num_head=n_heads_pair, transpose=False)
+        self.pair_attention2 = GridSelfAttention(c_pair=c_pair, num_head=n_heads_pair, transpose=True)
+        self.pair_transition = Transition(c_x=c_pair)
+
+    def forward(self, msa, pair, msa_mask, pair_mask):
+        _require_hip_backends()
+        return evoformer_block_hip(self, msa, pair, msa_mask, pair_mask)
