@@ -176,7 +176,7 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
                                 void *workspace, int64_t workspace_bytes, void *stream);
 
 /* Scratch bytes of xfh_triangle_multiplication_noalloc on each device (128 MiB: the bf16
- * c = 128 path up to n = 418, the fp32 path up to n = 161). */
+ * c = 128 path up to n = 415, the fp32 path up to n = 161). */
 #define XFH_NOALLOC_SCRATCH_BYTES ((int64_t)128 << 20)
 
 /* xfh_triangle_multiplication without a workspace argument: the same arguments, result and

@@ -96,18 +96,14 @@ struct TriMulPlan {
 
 static bool trimul_fast_path(int64_t c, int dtype) { return dtype == XFH_BF16 && c == 128; }
 
-// Channel planes of the contraction's operands and result, in elements (the result planes
-// start 16-byte aligned, so the output kernel reads them in 16-byte pieces for every n).
-static int64_t operand_plane(int64_t n) { return n * contraction_ld(n); }
-static int64_t result_plane(int64_t n) { return align_up(n * n, int64_t(8)); }
 
 static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int dtype, int out_dtype) {
   const int64_t es = dsize(dtype), plane = n * n;
   std::memset(&p, 0, sizeof(p));
   if (trimul_fast_path(c, dtype)) {
-    p.left = cv.take(operand_plane(n) * c * es);
-    p.right = cv.take(operand_plane(n) * c * es);
-    p.contracted = cv.take(result_plane(n) * c * es);
+    p.left = cv.take(contraction_operand_elems(n, c) * es);
+    p.right = cv.take(contraction_operand_elems(n, c) * es);
+    p.contracted = cv.take(contraction_result_elems(n, c) * es);
     return cv.used;
   }
   p.normed = cv.take(plane * c * es);
@@ -402,18 +398,15 @@ int xfh_triangle_multiplication(const void *pair, int pair_dtype, const void *ma
     pa.w_proj = static_cast<const bf16 *>(proj_w); pa.w_gate = static_cast<const bf16 *>(gate_w);
     pa.left = static_cast<bf16 *>(p.left); pa.right = static_cast<bf16 *>(p.right);
     pa.n = int(n); pa.ld = int(contraction_ld(n)); pa.outgoing = outgoing;
-    pa.plane = operand_plane(n);
     XFH_TRY(trimul_project(pa, pair_dtype, s));
     ContractionArgs ca;
     ca.left = static_cast<const bf16 *>(p.left);
     ca.right = static_cast<const bf16 *>(p.right);
     ca.out = static_cast<bf16 *>(p.contracted);
     ca.n = int(n); ca.ld = int(contraction_ld(n)); ca.channels = int(c);
-    ca.op_plane = operand_plane(n); ca.out_plane = result_plane(n);
     XFH_TRY(contraction(ca, s));
     TriOutputArgs oa;
     oa.pair = pair; oa.contracted = static_cast<const bf16 *>(p.contracted);
-    oa.c_plane = result_plane(n);
     oa.ln_in_w = left_w; oa.ln_in_b = left_b; oa.eps_in = left_eps;
     oa.ln_c_w = center_w; oa.ln_c_b = center_b; oa.eps_c = center_eps;
     oa.w_gating = static_cast<const bf16 *>(gating_w); oa.w_out = static_cast<const bf16 *>(out_w);

@@ -3,8 +3,10 @@
 // of xfold/nn/triangle_multiplication.py:96 for both directions (the operand layouts are
 // prepared by trimul_project).
 //
-// Operands: L, R [channels][n][ld] bf16, ld = contraction_ld(n) (a multiple of 32), with
-// zeros in the columns t in [n, ld) so that the last k-step needs no bounds.
+// Operands: L, R in the blocked operand layout (kernels.h): 16 rows x 32 t of one channel
+// are one contiguous 1 KB block, ld = contraction_ld(n), zeros for t in [n, ld) so that the
+// last k-step needs no bounds. The result goes to the blocked result layout: 16 pair
+// positions' channels contiguous.
 //
 // Tiling: 192 x 192 output tile per workgroup, 4 wavefronts in a 2 x 2 grid each owning
 // 96 x 96 (6 x 6 MFMA 16x16x32 tiles). Per k-step of 32 both 192 x 32 operand tiles go
@@ -14,7 +16,8 @@
 // c ^ ((r >> 2) & 3)), so the 16 rows of an MFMA operand read hit distinct bank groups.
 // The MFMA takes R rows as its A operand so that a lane ends up with four consecutive j
 // of one i and writes them as one 8-byte store. Channels are numbered so that each XCD
-// works through a contiguous run of tiles (their operands stay in that XCD's L2).
+// works through a contiguous run of tiles: the workgroups in flight on an XCD cover a few
+// consecutive channels, whose k-slices share 128-byte lines and DRAM pages.
 #include "common.h"
 #include "kernels.h"
 
@@ -48,11 +51,10 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wi = wave >> 1, wj = wave & 1, col = lane & 15, grp = lane >> 4;
-  const int64_t opsize = a.op_plane;
-  const bf16 *L = a.left + ch * opsize;
-  const bf16 *R = a.right + ch * opsize;
+  // k-step s of row g of channel ch at op_offset(n, c, ch, g, 0) + s * step_stride.
+  const int64_t step_stride = op_step_stride(n, a.channels);
 
-  // Piece p of a k-step: operand p / 12 (L, R), rows 16 (p % 12) .. +15; lane -> row
+  // Piece p of a k-step: operand p / 12 (L, R), rows 16 (p % 12) .. +15 (one 1 KB block); lane -> row
   // 16 (p % 12) + lane / 4, LDS slot lane % 4 holding chunk (lane % 4) ^ ((lane >> 4) & 3).
   // Rows beyond n read row n-1 (their results are never stored).
   const int chunk = (lane & 3) ^ ((lane >> 4) & 3);
@@ -62,14 +64,14 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
     const int p = wave + 4 * j;
     const int row = (p % 12) * 16 + (lane >> 2);
     const int g = (p < 12 ? i0 : j0) + row;
-    src[j] = (p < 12 ? L : R) + int64_t(g < n ? g : n - 1) * ld + chunk * 8;
+    src[j] = (p < 12 ? a.left : a.right) + op_offset(n, a.channels, int(ch), g < n ? g : n - 1, 0) + chunk * 8;
   }
   auto issue = [&](int step, int slot) {
 #pragma unroll
     for (int j = 0; j < PIECES / 4; ++j) {
       const int p = wave + 4 * j;
       bf16 *dst = lds + slot * SLOT_ELEMS + (p < 12 ? 0 : OP_ELEMS) + (p % 12) * 16 * TK;
-      __builtin_amdgcn_global_load_lds((global_void *)(src[j] + step * TK), (lds_void *)dst, 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((global_void *)(src[j] + step * step_stride), (lds_void *)dst, 16, 0, 0);
     }
   };
 
@@ -107,9 +109,10 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
     }
   }
 
-  // acc[x][y][e] = out[i = i0 + wi*96 + y*16 + col][j = j0 + wj*96 + x*16 + grp*4 + e]
-  bf16 *O = a.out + ch * a.out_plane;
-  const bool vec = (n % 4) == 0;
+  // acc[x][y][e] = out[i = i0 + wi*96 + y*16 + col][j = j0 + wj*96 + x*16 + grp*4 + e],
+  // pair position pos = i n + j at res_offset (16 positions' channels contiguous).
+  auto at = [&](int64_t pos) { return a.out + res_offset(a.channels, int(ch), pos); };
+  const bool vec = (n % 4) == 0;                    // then pos % 4 == 0: 4 positions in one block
 #pragma unroll
   for (int y = 0; y < NT; ++y) {
     const int i = i0 + wi * WT + y * 16 + col;
@@ -117,16 +120,16 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
 #pragma unroll
     for (int x = 0; x < NT; ++x) {
       const int j = j0 + wj * WT + x * 16 + grp * 4;
-      bf16 *dst = O + int64_t(i) * n + j;
+      const int64_t pos = int64_t(i) * n + j;
       if (vec && j + 4 <= n) {
         bf16x4 v;
 #pragma unroll
         for (int e = 0; e < 4; ++e) v[e] = bf16(acc[x][y][e]);
-        *reinterpret_cast<bf16x4 *>(dst) = v;
+        *reinterpret_cast<bf16x4 *>(at(pos)) = v;
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (j + e < n) dst[e] = bf16(acc[x][y][e]);
+          if (j + e < n) *at(pos + e) = bf16(acc[x][y][e]);
       }
     }
   }
@@ -135,12 +138,16 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
 }  // namespace
 
 int64_t contraction_ld(int64_t n) { return align_up(n, TK); }
+int64_t contraction_operand_elems(int64_t n, int64_t channels) {
+  return (contraction_ld(n) / TK) * op_step_stride(n, int(channels));
+}
+int64_t contraction_result_elems(int64_t n, int64_t channels) {
+  return ceil_div(n * n, 16) * res_block_stride(int(channels));
+}
 
 int contraction(const ContractionArgs &a, hipStream_t s) {
   if (a.n == 0 || a.channels == 0) return XFH_OK;
   if (a.ld != contraction_ld(a.n)) return fail(XFH_EINVAL, "contraction: operand rows must be padded to 32");
-  if (a.op_plane < int64_t(a.n) * a.ld || a.out_plane < int64_t(a.n) * a.n || a.op_plane % 8 || a.out_plane % 8)
-    return fail(XFH_EINVAL, "contraction: channel planes overlap or are not 16-byte aligned");
   const int64_t tiles = ceil_div(a.n, TB);
   const int64_t total = tiles * tiles * a.channels;
   const int64_t grid = ceil_div(total, 8) * 8;

@@ -138,14 +138,12 @@ struct TriProjectArgs {
   const float *ln_w, *ln_b;
   float eps;
   const bf16 *w_proj, *w_gate;  // [2c][c] each (nn.Linear layout)
-  bf16 *left, *right;        // [c][n][ld] contraction operands (contraction_ld), zero-padded
-  int64_t plane;             // elements from one channel's operand plane to the next (>= n ld)
+  bf16 *left, *right;        // contraction operands in the blocked operand layout, zero-padded
   int n, ld, outgoing;
 };
 struct TriOutputArgs {
   const void *pair;
-  const bf16 *contracted;    // [c][n][n], planes c_plane elements apart
-  int64_t c_plane;
+  const bf16 *contracted;    // contraction result in the blocked result layout
   const float *ln_in_w, *ln_in_b;
   float eps_in;
   const float *ln_c_w, *ln_c_b;
@@ -167,13 +165,39 @@ struct TransitionArgs {
 };
 int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStream_t s);
 
+// Layouts of the triangle multiplication's contraction (c = channels, ld = contraction_ld(n)):
+//   operand (left, right): element (ch, i, t) of the per-channel [n][ld] matrices in blocks of
+//     16 rows x 32 t (1 KB): block (t/32, i/16) holds the blocks of all channels together,
+//     element at ((t/32) * G + i/16) * op_group_stride + ch * 512 + (i % 16) * 32 + t % 32,
+//     G = ceil(n/16); zero for t >= n;
+//   result: element (ch, pos = i*n + j) at (pos/16) * res_block_stride + ch * 16 + pos % 16:
+//     16 pair positions, all channels of them contiguous (4 KB).
+// The contraction reads each k-step of 16 rows as one contiguous 1 KB piece; trimul_project's
+// wavefronts write neighbouring grid lines of one k-slice at the same time (64-byte pieces
+// that fill whole rows of a block); trimul_output reads 16 positions' channels as one
+// contiguous block. Against channel-major [c][n][ld] operands and [c][n*n] results this
+// took the contraction from 167 to 155 us and trimul_output from 123 to 101 us at n = 768.
+// The result blocks are padded by 128 bytes so that the contraction's stores to the 16
+// rows i of a tile are not a power of two apart.
+constexpr int kOpGroupPad = 0, kResPad = 64;    // elements (multiples of 8)
+__host__ __device__ inline int64_t op_groups(int64_t n) { return (n + 15) / 16; }
+__host__ __device__ inline int64_t op_group_stride(int c) { return int64_t(c) * 512 + kOpGroupPad; }
+__host__ __device__ inline int64_t op_step_stride(int64_t n, int c) { return op_groups(n) * op_group_stride(c); }
+__host__ __device__ inline int64_t op_offset(int64_t n, int c, int ch, int64_t i, int64_t s) {
+  return (s * op_groups(n) + (i >> 4)) * op_group_stride(c) + int64_t(ch) * 512 + (i & 15) * 32;
+}
+__host__ __device__ inline int64_t res_block_stride(int c) { return int64_t(c) * 16 + kResPad; }
+__host__ __device__ inline int64_t res_offset(int c, int ch, int64_t pos) {
+  return (pos >> 4) * res_block_stride(c) + int64_t(ch) * 16 + (pos & 15);
+}
 struct ContractionArgs {
-  const bf16 *left, *right;  // [channels][n][ld], k-contiguous rows, zero for k >= n
-  bf16 *out;                 // [channels][n][n]
-  int64_t op_plane, out_plane;  // elements between channel planes (>= n ld, >= n n)
+  const bf16 *left, *right;  // blocked operand layout
+  bf16 *out;                 // blocked result layout
   int n, ld, channels;
 };
 int64_t contraction_ld(int64_t n);
+int64_t contraction_operand_elems(int64_t n, int64_t channels);
+int64_t contraction_result_elems(int64_t n, int64_t channels);
 int contraction(const ContractionArgs &a, hipStream_t s);
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s);
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s);

@@ -1,6 +1,6 @@
 // xfh_triangle_multiplication_noalloc: the triangle multiplication entry point for callers
 // that cannot allocate device memory (code under HIP graph capture, serving loops that
-// forbid allocation). Its scratch (the contraction's operand and result planes, or the
+// forbid allocation). Its scratch (the contraction's operands and result, or the
 // general path's intermediates) lives in one file-scope device array instead of a
 // caller-provided workspace; every other argument and the result are those of
 // xfh_triangle_multiplication, whose kernels it runs.

@@ -2,9 +2,9 @@
 // contraction (xfold/nn/triangle_multiplication.py:71-105):
 //
 //   trimul_project: LN_in(z) -> [projection | gate] (one GEMM over both weights' rows) ->
-//       mask * proj * sigmoid(gate) -> channel 2k = a_k, 2k+1 = b_k -> written channel-major
-//       in the contraction's operand layouts (left/right, see triangle.hip).
-//   trimul_output: centre LN over the channel-major contraction result -> output_projection,
+//       mask * proj * sigmoid(gate) -> channel 2k = a_k, 2k+1 = b_k -> written in the
+//       contraction's blocked operand layout (left/right; kernels.h).
+//   trimul_output: centre LN over the blocked contraction result -> output_projection,
 //       times sigmoid(gating_linear(LN_in(z))) (recomputed from z, which this kernel reads
 //       anyway for the residual) -> z += update (or update stored).
 //
@@ -32,9 +32,10 @@ using namespace panel;
 //   out    = p * sigmoid(g) * mask             channel 2k -> a_k, 2k + 1 -> b_k
 // With RT = 2, row m of row tile rt is position y0 + 8 (m / 4) + 4 rt + m % 4, so that the
 // lane that holds channel c of rows 4 g .. 4 g + 3 in both tiles has positions y0 + 8 g .. + 7
-// of c: one 16-byte store into the channel-major operand row. RT = 1 (row m = position
-// y0 + m, 8-byte stores) halves the unit for grids too small to give every wavefront
-// several 32-position units.
+// of c: one 16-byte store into the blocked operand layout (kernels.h), where the 16 grid
+// lines x of one row group and the 32 positions of a k-slice of all channels form one block.
+// RT = 1 (row m = position y0 + m, 8-byte stores) halves the unit for grids too small to
+// give every wavefront several 32-position units.
 constexpr int PROJ = 2 * K;          // projection (and gate) output channels
 
 template <typename TIN, int RT>
@@ -52,12 +53,14 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
   sg.load([&](int row) { return a.w_gate + row * K; }, false);
   sl.load(a.ln_w, a.ln_b);
 
+  // Unit u = (grid line x = u % n, positions y0 = (u / n) UP ..): the wavefronts of a
+  // workgroup take neighbouring grid lines of one k-slice, whose operand rows are
+  // neighbours in the blocked layout.
   const int n = a.n, cpr = a.ld / UP;               // units per grid line
   const int units = n * cpr;                        // < 2^31 (n * ld fits in 32 bits)
   const int lane = threadIdx.x & 63, m = lane & 15, g = lane >> 4;
   const int waves = int(gridDim.x) * int(blockDim.x >> 6);
   const TIN *z = static_cast<const TIN *>(a.pair);
-  const int64_t plane = a.plane;
   // Pair position of grid-line entry (x, y): (x, y) outgoing, (y, x) incoming.
   auto pos_of = [&](int x, int y) -> int64_t { return a.outgoing ? int64_t(x) * n + y : int64_t(y) * n + x; };
 
@@ -66,7 +69,7 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
     float mrow[RT];                                 // mask of those rows (0 for y >= n)
   };
   auto fetch = [&](int u, Unit &w) {
-    const int x = u / cpr, y0 = (u - x * cpr) * UP;
+    const int y0 = (u / n) * UP, x = u - (u / n) * n;
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       const int y = y0 + row_y(rt, m);
@@ -98,9 +101,10 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
     for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int e = 0; e < 4; ++e) mk[4 * rt + e] = __shfl(cur.mrow[rt], 4 * g + e, 64);
-    const int x = u / cpr, y0 = (u - x * cpr) * UP;
+    const int y0 = (u / n) * UP, x = u - (u / n) * n;
     const int y_lane = y0 + 4 * RT * g;             // positions y_lane .. + 4 RT - 1
-    const int64_t row_off = int64_t(x) * a.ld + y_lane;
+    // k-slice y_lane / 32 of row x of channel 0; channel ch adds 512 ch.
+    const int64_t row_off = op_offset(n, K, 0, x, y_lane >> 5) + (y_lane & 31);
     const bool pad = y0 + UP > n;
 #pragma unroll 1
     for (int t = 0; t < PROJ / 16; ++t) {
@@ -129,7 +133,7 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
       }
       const int p = 16 * t + m;                     // projection channel
       const bool is_a = (p & 1) == 0;
-      bf16 *dst = ((a.outgoing != 0) == is_a ? a.left : a.right) + int64_t(p >> 1) * plane + row_off;
+      bf16 *dst = ((a.outgoing != 0) == is_a ? a.left : a.right) + (p >> 1) * 512 + row_off;
       *reinterpret_cast<Out *>(dst) = o;
     }
     cur = next;
@@ -139,9 +143,9 @@ __global__ __launch_bounds__(512, 1) void trimul_project_kernel(TriProjectArgs a
 // trimul_output, one wavefront per 16 positions at a time (rowstep.h), weights resident in
 // LDS, activations in registers, no barriers after the weights are in:
 //   gate^T = Wg . LN_in(z)^T                  (K-layout z -> O-layout gate logits)
-//   c      = contraction result, channel-major: 16-byte loads of 8 positions of a channel
-//            are an MFMA A fragment, times an identity B (either k-half) they land in
-//            O-layout (exact)
+//   c      = contraction result, blocked (kernels.h): the 16 positions' channels are one
+//            contiguous 4 KB block; 16-byte loads of 8 positions of a channel are an MFMA A
+//            fragment, times an identity B (either k-half) they land in O-layout (exact)
 //   y      = bf16(LN_c(c))                    (statistics over the 4 lanes of a position)
 //   u^T    = Wout . y^T                       (Wout in kperm order)
 //   z     += bf16(u * sigmoid(gate))
@@ -182,9 +186,9 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
     const int64_t p0 = st * 16 + 8 * (g & 1);
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const bf16 *src = a.contracted + int64_t(16 * (q + 4 * (g >> 1)) + r) * a.c_plane + p0;
+      const bf16 *src = a.contracted + res_offset(K, 16 * (q + 4 * (g >> 1)) + r, p0);
       bf16x8 v = {};
-      if (p0 + 8 <= npos) {                      // planes start 16-byte aligned
+      if (p0 + 8 <= npos) {
         v = *reinterpret_cast<const bf16x8 *>(src);
       } else {
 #pragma unroll
@@ -290,9 +294,7 @@ __global__ __launch_bounds__(512, 1) void trimul_output_kernel(TriOutputArgs a) 
 }  // namespace
 
 int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
-  if (a.ld % 32 != 0 || a.ld < a.n) return fail(XFH_EINVAL, "trimul_project: ld must be a multiple of 32, >= n");
-  if (a.plane < int64_t(a.n) * a.ld || a.plane % 8)
-    return fail(XFH_EINVAL, "trimul_project: operand planes overlap or are not 16-byte aligned");
+  if (a.ld != contraction_ld(a.n)) return fail(XFH_EINVAL, "trimul_project: ld must be contraction_ld(n)");
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   // 32-position units unless that leaves fewer than four per wavefront (the last round of
@@ -314,8 +316,6 @@ int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
 
 int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStream_t s) {
   const int64_t steps = ceil_div(int64_t(a.n) * a.n, 16);
-  if (a.c_plane < int64_t(a.n) * a.n || a.c_plane % 8)
-    return fail(XFH_EINVAL, "trimul_output: result planes overlap or are not 16-byte aligned");
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(steps, 8, cus)));
