@@ -253,6 +253,17 @@ int xfh_msa_attention(const void *msa, int msa_dtype, const void *mask, int mask
                       const void *gating_w, const void *out_w, int dtype, void *out, int out_dtype, int accumulate,
                       void *workspace, int64_t workspace_bytes, void *stream);
 
+/* Logit bias of the atom CrossAttention, fp32 out [batch, heads, nq, nk] contiguous:
+ *   out[b, h, q, k] = pair_logits[b, h, q, k] + 1e9 * (mask_q[b, q] == 0 && mask_k[b, k] == 0)
+ * pair_logits strided (4 strides in elements, f32/bf16) or NULL (0); masks contiguous
+ * [batch, nq] / [batch, nk] (f32/bf16/bool) or NULL (all kept). The result is the bias of
+ * an xfh_dot_product_attention call with no mask. Replaces the bias construction of
+ * CrossAttention.forward (xfold/nn/diffusion_transformer.py:318-339), whose positive 1e9
+ * term makes a masked query attend to the masked keys only. */
+int xfh_cross_attention_bias(const void *pair_logits, int logits_dtype, const int64_t *strides,
+                             const void *mask_q, int mask_q_dtype, const void *mask_k, int mask_k_dtype,
+                             int64_t batch, int64_t heads, int64_t nq, int64_t nk, float *out, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -170,3 +170,53 @@ def msa_attention(msa, mask, pair, params, heads):
             gated = [avg[ch] * _sigmoid(gate[ch]) for ch in range(c)]
             out[s][q] = linear(gated, params["out"])
     return out
+
+
+def cross_attention(x_q, x_k, mask_q, mask_k, pair_logits, cond_q, cond_k, params, heads):
+    """CrossAttention (``xfold/nn/diffusion_transformer.py:275-350``) for one subset by
+    loops. x_q: [Q][C], x_k: [K][C], masks [Q] / [K], pair_logits [H][Q][K] or None,
+    cond_q [Q][S], cond_k [K][S]. AdaLN(x, c) = sigmoid(W_s LN_w(c) + b_s) * LN(x) + W_b LN_w(c);
+    logit = d^-0.5 q.k + 1e9 [both masked] + pair; out = sigmoid(W_z c_q + b_z) * W_t(avg * sigmoid(W_g x_q'))."""
+    c = len(x_q[0])
+    d = c // heads
+
+    def linear(x, w, b=None):
+        return [sum(w[o][t] * x[t] for t in range(len(x))) + (b[o] if b is not None else 0.0)
+                for o in range(len(w))]
+
+    def ada(x, cond, pre):
+        xn = layer_norm([x])[0]
+        cn = layer_norm([cond], params[pre + "cond_ln_w"])[0]
+        scale = linear(cn, params[pre + "scale_w"], params[pre + "scale_b"])
+        shift = linear(cn, params[pre + "shift_w"])
+        return [_sigmoid(scale[i]) * xn[i] + shift[i] for i in range(c)]
+
+    xq = [ada(x_q[i], cond_q[i], "q_") for i in range(len(x_q))]
+    xk = [ada(x_k[j], cond_k[j], "k_") for j in range(len(x_k))]
+    qs = [linear(x, params["q_w"], params["q_b"]) for x in xq]
+    ks = [linear(x, params["k_w"]) for x in xk]
+    vs = [linear(x, params["v_w"]) for x in xk]
+    out = []
+    for i in range(len(x_q)):
+        avg = [0.0] * c
+        for h in range(heads):
+            logits = []
+            for j in range(len(x_k)):
+                s = sum(qs[i][h * d + t] * d ** -0.5 * ks[j][h * d + t] for t in range(d))
+                if mask_q[i] == 0 and mask_k[j] == 0:
+                    s += 1e9
+                if pair_logits is not None:
+                    s += pair_logits[h][i][j]
+                logits.append(s)
+            top = max(logits)
+            ex = [math.exp(s - top) for s in logits]
+            total = sum(ex)
+            for j in range(len(x_k)):
+                for t in range(d):
+                    avg[h * d + t] += ex[j] / total * vs[j][h * d + t]
+        gate = linear(xq[i], params["gate_w"])
+        gated = [avg[ch] * _sigmoid(gate[ch]) for ch in range(c)]
+        zero = linear(cond_q[i], params["zero_w"], params["zero_b"])
+        upd = linear(gated, params["t2_w"])
+        out.append([_sigmoid(zero[ch]) * upd[ch] for ch in range(c)])
+    return out

@@ -426,6 +426,52 @@ class SelfAttention(nn.Module):
         return self.adaptive_zero_init(weighted, single_cond)
 
 
+class CrossAttention(nn.Module):
+    """``xfold/nn/diffusion_transformer.py:275-350``: attention of atom-query subsets over
+    atom-key subsets (x_q [..., Q, key_dim], x_k [..., K, key_dim], masks [..., Q] / [..., K]).
+
+    q = q_projection(AdaLN_q(x_q, cond_q)) (with bias), k and v from AdaLN_k(x_k, cond_k);
+    logits[h, q, k] = (q_scale q) . k + 1e9 [mask_q[q] == 0 and mask_k[k] == 0] (+ pair_logits)
+    (:318-339): the 1e9 term is positive, so a masked query attends to the masked keys only
+    and an unmasked query to every key. Softmax over keys, gate with
+    sigmoid(gating_query(AdaLN_q(x_q))), AdaLNZero conditioned on cond_q (:341-350).
+    """
+
+    def __init__(self, key_dim: int = 128, value_dim: int = 128, c_single_cond: int = 128,
+                 num_head: int = 4) -> None:
+        super().__init__()
+        self.key_dim = key_dim
+        self.value_dim = value_dim
+        self.c_single_cond = c_single_cond
+        self.num_head = num_head
+        self.key_dim_per_head = key_dim // num_head
+        self.value_dim_per_head = value_dim // num_head
+        self.q_scale = self.key_dim_per_head ** -0.5
+        self.q_adaptive_layernorm = AdaptiveLayerNorm(key_dim, c_single_cond, use_single_cond=True)
+        self.k_adaptive_layernorm = AdaptiveLayerNorm(key_dim, c_single_cond, use_single_cond=True)
+        self.q_projection = nn.Linear(key_dim, key_dim, bias=True)
+        self.k_projection = nn.Linear(key_dim, key_dim, bias=False)
+        self.v_projection = nn.Linear(value_dim, value_dim, bias=False)
+        self.gating_query = nn.Linear(key_dim, value_dim, bias=False)
+        self.adaptive_zero_init = AdaLNZero(value_dim, value_dim, key_dim, use_single_cond=True)
+
+    def forward(self, x_q, x_k, mask_q, mask_k, pair_logits=None, single_cond_q=None, single_cond_k=None):
+        both_masked = ((mask_q == 0).unsqueeze(-1) & (mask_k == 0).unsqueeze(-2)).unsqueeze(-3)
+        xq = self.q_adaptive_layernorm(x_q, single_cond_q)
+        xk = self.k_adaptive_layernorm(x_k, single_cond_k)
+        h = self.num_head
+        q = self.q_projection(xq).unflatten(-1, (h, self.key_dim_per_head))
+        k = self.k_projection(xk).unflatten(-1, (h, self.key_dim_per_head))
+        logits = torch.einsum("...qhc,...khc->...hqk", q * self.q_scale, k) + 1e9 * both_masked
+        if pair_logits is not None:
+            logits = logits + pair_logits
+        weights = torch.softmax(logits, dim=-1)
+        v = self.v_projection(xk).unflatten(-1, (h, self.value_dim_per_head))
+        avg = torch.einsum("...hqk,...khc->...qhc", weights, v).flatten(-2)
+        avg = avg * torch.sigmoid(self.gating_query(xq))
+        return self.adaptive_zero_init(avg, single_cond_q)
+
+
 class PairformerBlock(nn.Module):
     """``xfold/nn/pairformer.py:26-114``.
 

@@ -9,8 +9,8 @@ with ``xfold_cpu_amd.synthetic.init_module_`` (LayerNorm affine jittered), runs 
 seeded inputs in fp32 and under CPU bf16 autocast, and saves inputs, the state_dict and
 outputs as ``.npz`` (data only). It covers the compositions that no closed form pins:
 grid self-attention (both nodes), Transition, SelfAttention with and without
-conditioning, DiffusionTransition, PairformerBlock, DiffusionTransformer and
-EvoformerBlock (with OuterProductMean and MSAAttention inside).
+conditioning, DiffusionTransition, PairformerBlock, DiffusionTransformer,
+EvoformerBlock (with OuterProductMean and MSAAttention inside) and the atom CrossAttention.
 """
 
 from __future__ import annotations
@@ -51,7 +51,7 @@ def main(reference: str):
     sys.path.insert(0, reference)
     from xfold.fastnn import config
     from xfold.nn.attention import GridSelfAttention
-    from xfold.nn.diffusion_transformer import DiffusionTransformer, DiffusionTransition, SelfAttention
+    from xfold.nn.diffusion_transformer import CrossAttention, DiffusionTransformer, DiffusionTransition, SelfAttention
     from xfold.nn.pairformer import EvoformerBlock, PairformerBlock
     from xfold.nn.primitives import Transition
 
@@ -162,6 +162,26 @@ def main(reference: str):
     save("evoformer_block", mod, args,
          {"msa": msa0, "pair": pair0, "msa_mask": msa_mask, "pair_mask": pmask},
          {"msa": msa, "pair": pair}, {"module": "EvoformerBlock"})
+
+    # CrossAttention (atom queries over atom keys, per subset): a masked query, masked keys
+    # (the positive 1e9 term then applies to the masked pairs) and pair logits.
+    subsets, nq, nk, c = 3, 4, 6, 32
+    args = dict(key_dim=c, value_dim=c, c_single_cond=c, num_head=4)
+    mod = init_module_(CrossAttention(**args).eval(), seed=9, ln_jitter=True)
+    x_q, x_k = randn(subsets, nq, c), randn(subsets, nk, c)
+    mask_q = torch.ones(subsets, nq)
+    mask_q[0, 3] = 0.0
+    mask_k = torch.ones(subsets, nk)
+    mask_k[0, 1] = 0.0
+    mask_k[2, 5] = 0.0
+    pair_logits = randn(subsets, 4, nq, nk)
+    cond_q, cond_k = randn(subsets, nq, c), randn(subsets, nk, c)
+    with torch.inference_mode():
+        out = mod(x_q, x_k, mask_q, mask_k, pair_logits, cond_q, cond_k)
+    save("cross_attention", mod, args,
+         {"x_q": x_q, "x_k": x_k, "mask_q": mask_q, "mask_k": mask_k, "pair_logits": pair_logits,
+          "single_cond_q": cond_q, "single_cond_k": cond_k},
+         {"out": out}, {"module": "CrossAttention"})
 
 
 if __name__ == "__main__":

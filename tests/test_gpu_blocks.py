@@ -34,6 +34,9 @@ def run_hip_fixture(name, device):
         elif kind == "PairformerBlock":
             pair, single = module(d["pair"].clone(), d["pair_mask"], d["single"].clone(), d["seq_mask"])
             got = {"pair": pair, "single": single}
+        elif kind == "CrossAttention":
+            got = {"out": module(d["x_q"], d["x_k"], d["mask_q"], d["mask_k"], d["pair_logits"],
+                                 d["single_cond_q"], d["single_cond_k"])}
         else:
             got = {"out": module(d["act"].clone(), d["mask"], d["single_cond"], d["pair_cond"])}
     return meta, got, outputs
@@ -41,7 +44,7 @@ def run_hip_fixture(name, device):
 
 @pytest.mark.parametrize("name", ["grid_attention_start", "grid_attention_end", "transition",
                                   "self_attention", "self_attention_cond", "diffusion_transition",
-                                  "pairformer_block", "diffusion_transformer"])
+                                  "pairformer_block", "diffusion_transformer", "cross_attention"])
 def test_golden_vectors_through_hip(device, name):
     """fp32 golden vectors written by the reference's own modules."""
     announce("golden", name)

@@ -173,6 +173,7 @@ MODULES = {
     "PairformerBlock": R.PairformerBlock,
     "DiffusionTransformer": R.DiffusionTransformer,
     "EvoformerBlock": R.EvoformerBlock,
+    "CrossAttention": R.CrossAttention,
 }
 
 
@@ -199,6 +200,9 @@ def run_oracle_on_fixture(name):
             msa, pair = module(inputs["msa"].clone(), inputs["pair"].clone(), inputs["msa_mask"],
                                inputs["pair_mask"])
             got = {"msa": msa, "pair": pair}
+        elif kind == "CrossAttention":
+            got = {"out": module(inputs["x_q"], inputs["x_k"], inputs["mask_q"], inputs["mask_k"],
+                                 inputs["pair_logits"], inputs["single_cond_q"], inputs["single_cond_k"])}
         else:
             got = {"out": module(inputs["act"].clone(), inputs["mask"], inputs["single_cond"],
                                  inputs["pair_cond"])}
@@ -208,7 +212,7 @@ def run_oracle_on_fixture(name):
 @pytest.mark.parametrize("name", ["grid_attention_start", "grid_attention_end", "transition",
                                   "self_attention", "self_attention_cond", "diffusion_transition",
                                   "pairformer_block", "pairformer_block_bf16", "diffusion_transformer",
-                                  "evoformer_block"])
+                                  "evoformer_block", "cross_attention"])
 def test_oracle_reproduces_reference_golden_vectors(name):
     meta, got, want = run_oracle_on_fixture(name)
     tol = 1e-6 if not meta.get("autocast") else 1e-2
@@ -379,3 +383,69 @@ def test_golden_catches_an_evoformer_order_mistake():
         msa += module.msa_attention1(msa, inputs["msa_mask"], pair_before)
         msa += module.msa_transition(msa)
     assert rel_err(msa, outputs["msa"]) > 1e-4
+
+
+def _cross_attention_params(module):
+    qa, ka, z = module.q_adaptive_layernorm, module.k_adaptive_layernorm, module.adaptive_zero_init
+    params = {}
+    for pre, a in (("q_", qa), ("k_", ka)):
+        params[pre + "cond_ln_w"] = _nested(a.single_cond_layer_norm.weight)
+        params[pre + "scale_w"] = _nested(a.single_cond_scale.weight)
+        params[pre + "scale_b"] = _nested(a.single_cond_scale.bias)
+        params[pre + "shift_w"] = _nested(a.single_cond_bias.weight)
+    params.update(q_w=_nested(module.q_projection.weight), q_b=_nested(module.q_projection.bias),
+                  k_w=_nested(module.k_projection.weight), v_w=_nested(module.v_projection.weight),
+                  gate_w=_nested(module.gating_query.weight), zero_w=_nested(z.adaptive_zero_cond.weight),
+                  zero_b=_nested(z.adaptive_zero_cond.bias), t2_w=_nested(z.transition2.weight))
+    return params
+
+
+@pytest.mark.parametrize("with_pair", [True, False])
+def test_cross_attention_matches_brute_force(with_pair):
+    """CrossAttention against plain loops, subset by subset: a masked query (which then
+    attends to the masked keys only, through the positive 1e9 term), masked keys seen by
+    the unmasked queries, with and without pair logits."""
+    from xfold_cpu_amd.synthetic import init_module_
+    module = init_module_(R.CrossAttention(key_dim=8, value_dim=8, c_single_cond=8, num_head=2).eval(),
+                          seed=4, ln_jitter=True).double()
+    g = torch.Generator().manual_seed(4)
+    x_q = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
+    x_k = torch.randn(2, 5, 8, generator=g, dtype=torch.float64)
+    cq = torch.randn(2, 3, 8, generator=g, dtype=torch.float64)
+    ck = torch.randn(2, 5, 8, generator=g, dtype=torch.float64)
+    mq = torch.ones(2, 3, dtype=torch.float64)
+    mq[1, 0] = 0
+    mk = torch.ones(2, 5, dtype=torch.float64)
+    mk[1, 2] = 0
+    mk[1, 4] = 0
+    pl = torch.randn(2, 2, 3, 5, generator=g, dtype=torch.float64) if with_pair else None
+    with torch.no_grad():
+        got = module(x_q, x_k, mq, mk, pl, cq, ck)
+    params = _cross_attention_params(module)
+    for s in range(2):
+        want = torch.tensor(brute.cross_attention(_nested(x_q[s]), _nested(x_k[s]), _nested(mq[s]), _nested(mk[s]),
+                                                  None if pl is None else _nested(pl[s]), _nested(cq[s]),
+                                                  _nested(ck[s]), params, 2), dtype=torch.float64)
+        assert rel_err(got[s], want) < 1e-10
+
+
+def test_golden_catches_a_negative_cross_attention_mask():
+    """Reading the 1e9 term as the usual -1e9 fill of masked keys (a plausible restatement
+    mistake) fails the reference's golden vector: its masked query attends to masked keys."""
+    meta, inputs, params, outputs = load_fixture("cross_attention")
+    module = R.CrossAttention(**meta["args"]).eval()
+    module.load_state_dict(params)
+    with torch.inference_mode():
+        mq, mk = inputs["mask_q"], inputs["mask_k"]
+        xq = module.q_adaptive_layernorm(inputs["x_q"], inputs["single_cond_q"])
+        xk = module.k_adaptive_layernorm(inputs["x_k"], inputs["single_cond_k"])
+        q = module.q_projection(xq).unflatten(-1, (4, -1)) * module.q_scale
+        k = module.k_projection(xk).unflatten(-1, (4, -1))
+        logits = torch.einsum("...qhc,...khc->...hqk", q, k) + inputs["pair_logits"]
+        logits = logits - 1e9 * (mk == 0)[:, None, None, :]
+        w = torch.softmax(logits, -1)
+        v = module.v_projection(xk).unflatten(-1, (4, -1))
+        avg = torch.einsum("...hqk,...khc->...qhc", w, v).flatten(-2)
+        avg = avg * torch.sigmoid(module.gating_query(xq))
+        wrong = module.adaptive_zero_init(avg, inputs["single_cond_q"])
+    assert rel_err(wrong, outputs["out"]) > 1e-3

@@ -4,7 +4,8 @@
 // logit is replaced by exactly -1e9 (so a fully masked row averages v uniformly over all
 // keys); softmax over keys; @ v. The logits never exist in memory: each workgroup owns 64
 // queries of one (batch, head), walks the keys in blocks of 64 and keeps a running max and
-// sum (online softmax, base-2: log2(e) is folded into q, the bias and the -1e9 fill).
+// sum (online softmax, base-2: log2(e) is folded into the q.k scale, the bias and the -1e9
+// fill).
 //
 // MFMA formulation (16x16 tiles): the kernel computes S^T = K Q^T so that after the MFMA a
 // lane holds four keys of ONE query (column l%16). That is exactly the B-operand layout of
@@ -41,7 +42,8 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
   const T *kp = static_cast<const T *>(a.k) + b * a.ks[0] + h * a.ks[1];
   const T *vp = static_cast<const T *>(a.v) + b * a.vs[0] + h * a.vs[1];
 
-  // Q^T fragments (B operand): lane supplies d = step*32 + 8*grp + s of its query.
+  // Q^T fragments (B operand): lane supplies d = step*32 + 8*grp + s of its query, as
+  // stored (the scale goes onto the fp32 products, so q is not rounded a second time).
   typename Frag<T>::type qf[DP / 32];
   const float qscale = a.scale * kLog2e;
 #pragma unroll
@@ -50,8 +52,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       const int64_t d = st * 32 + grp * 8 + s;
-      float val = (qvalid && d < a.D) ? to_f32(qp[query * a.qs[2] + d]) * qscale : 0.f;
-      tmp[s] = from_f32<T>(val);
+      tmp[s] = (qvalid && d < a.D) ? qp[query * a.qs[2] + d] : T(0);
     }
     __builtin_memcpy(&qf[st], tmp, sizeof(tmp));
   }
@@ -94,7 +95,7 @@ __global__ __launch_bounds__(256) void attention_kernel(AttentionArgs a) {
         acc = mfma16(kf, qf[st], acc);
       }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) sv[kt][e] = acc[e];
+      for (int e = 0; e < 4; ++e) sv[kt][e] = acc[e] * qscale;
     }
 
     float bmax = -INFINITY;

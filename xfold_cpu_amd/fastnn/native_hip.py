@@ -72,6 +72,7 @@ SIGNATURES = {
     "xfh_msa_attention_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64, _i]),
     "xfh_msa_attention": (_i, [_p, _i, _p, _i, _p, _i, _i64, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p, _f,
                                _p, _p, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
+    "xfh_cross_attention_bias": (_i, [_p, _i, _pi64, _p, _i, _p, _i, _i64, _i64, _i64, _i64, _p, _p]),
 }
 
 

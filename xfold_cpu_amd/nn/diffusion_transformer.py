@@ -1,7 +1,7 @@
 """Diffusion-transformer modules with the reference's constructors, parameter names and
 call signatures (``xfold/nn/diffusion_transformer.py:27-272``), running on the HIP backend:
 AdaptiveLayerNorm, AdaLNZero, DiffusionTransition, SelfAttention (also the Pairformer's
-single-track attention) and DiffusionTransformer.
+single-track attention), DiffusionTransformer and the atom CrossAttention (:275-350).
 
 The ``*_hip`` functions take any module carrying the reference's parameters. Activations
 may carry a leading sample dim ([S, N, c]); conditioning tensors ([N, c_cond]) and pair
@@ -11,6 +11,7 @@ sample at a time.
 
 from __future__ import annotations
 
+import ctypes
 from typing import Optional
 
 import torch
@@ -41,9 +42,11 @@ def _adaptive_layer_norm(aln: nn.Module, x: torch.Tensor, single_cond: Optional[
     cln = aln.single_cond_layer_norm
     cond = ops.layer_norm(single_cond, cln.normalized_shape, cln.weight, cln.bias, cln.eps,
                           out_dtype=dtype, owner=cln)
+    # scale and shift stay fp32 (one rounding fewer before the sigmoid and the add).
     scale = ops.linear(cond, nh.linear_weight(aln, "single_cond_scale", dtype),
-                       aln.single_cond_scale.bias, dtype)
-    shift = ops.linear(cond, nh.linear_weight(aln, "single_cond_bias", dtype), None, dtype)
+                       aln.single_cond_scale.bias, dtype, out_dtype=torch.float32)
+    shift = ops.linear(cond, nh.linear_weight(aln, "single_cond_bias", dtype), None, dtype,
+                       out_dtype=torch.float32)
     return ops.adaptive_layer_norm(x, scale, shift, aln.layer_norm.eps, out_dtype=out_dtype)
 
 
@@ -370,6 +373,85 @@ class SelfAttention(nn.Module):
     def forward(self, x, mask, pair_logits=None, single_cond=None):
         _require(fastnn_config.dot_product_attention_implementation, "dot_product_attention_implementation")
         return self_attention_hip(self, x, mask, pair_logits, single_cond)
+
+
+def cross_attention_hip(module: nn.Module, x_q: torch.Tensor, x_k: torch.Tensor, mask_q: torch.Tensor,
+                        mask_k: torch.Tensor, pair_logits: Optional[torch.Tensor] = None,
+                        single_cond_q: Optional[torch.Tensor] = None, single_cond_k: Optional[torch.Tensor] = None,
+                        accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``CrossAttention.forward`` (``diffusion_transformer.py:304-350``) for x_q [..., Q, c],
+    x_k [..., K, c] with masks [..., Q] / [..., K] and pair_logits broadcastable to
+    [..., H, Q, K]: the q/k adaptive LayerNorms, the q and fused k|v projections, one
+    attention over all subsets whose fp32 bias (pair logits + the reference's positive 1e9
+    on pairs of a masked query and a masked key) comes from xfh_cross_attention_bias, the
+    sigmoid gate as the gating Linear's epilogue and the conditioned AdaLNZero."""
+    if mask_q.dim() != x_q.dim() - 1 or mask_k.dim() != x_k.dim() - 1:
+        raise ValueError(f"CrossAttention: masks must drop the channel dim of x ({tuple(mask_q.shape)}, "
+                         f"{tuple(x_q.shape)}; {tuple(mask_k.shape)}, {tuple(x_k.shape)})")
+    nh.check_gpu_inference(x_q, x_k, mask_q, mask_k, pair_logits, single_cond_q, single_cond_k,
+                           *module.parameters())
+    names = ("q_projection", "k_projection", "v_projection", "gating_query")
+    dtype = nh.compute_dtype(x_q, *(getattr(module, n).weight for n in names))
+    lead, nq, nk = tuple(x_q.shape[:-2]), x_q.shape[-2], x_k.shape[-2]
+    if tuple(x_k.shape[:-2]) != lead:
+        raise ValueError("CrossAttention: x_q and x_k must share their leading (subset) dims")
+    batch = 1
+    for d in lead:
+        batch *= d
+    h, dk, dv = module.num_head, module.key_dim_per_head, module.value_dim_per_head
+    kd, vd = module.key_dim, module.value_dim
+    if accumulate_into is not None and (not accumulate_into.is_contiguous() or
+                                        tuple(accumulate_into.shape) != lead + (nq, vd)):
+        raise ValueError("accumulate_into must be a contiguous [..., Q, value_dim] tensor")
+    xq = _adaptive_layer_norm(module.q_adaptive_layernorm, x_q, single_cond_q, dtype)
+    xk = _adaptive_layer_norm(module.k_adaptive_layernorm, x_k, single_cond_k, dtype)
+    q = ops.linear(xq, nh.linear_weight(module, "q_projection", dtype), module.q_projection.bias, dtype)
+    kv = ops.linear(xk, nh.fused_linear_weight(module, ("k_projection", "v_projection"), dtype), None, dtype)
+    q4 = torch.as_strided(q, (batch, h, nq, dk), (nq * kd, dk, kd, 1))
+    k4 = torch.as_strided(kv, (batch, h, nk, dk), (nk * (kd + vd), dk, kd + vd, 1))
+    v4 = torch.as_strided(kv, (batch, h, nk, dv), (nk * (kd + vd), dv, kd + vd, 1), kd)
+    mq, mq_code = nh.mask_arg(mask_q, lead + (nq,))
+    mk, mk_code = nh.mask_arg(mask_k, lead + (nk,))
+    bias = torch.empty((batch, h, nq, nk), dtype=torch.float32, device=x_q.device)
+    pl, pl_code, strides = None, nh.F32, None
+    if pair_logits is not None:
+        if pair_logits.dtype not in (torch.float32, torch.bfloat16):
+            raise ValueError("CrossAttention: pair_logits must be fp32 or bf16")
+        pl = pair_logits.expand(*lead, h, nq, nk).reshape(batch, h, nq, nk)
+        pl_code = nh.dtype_code(pl.dtype)
+        strides = (ctypes.c_int64 * 4)(*pl.stride())
+    nh.call("xfh_cross_attention_bias", nh.ptr(pl), pl_code, strides, nh.ptr(mq), mq_code, nh.ptr(mk), mk_code,
+            batch, h, nq, nk, nh.ptr(bias), nh.stream_of(x_q.device))
+    o = torch.empty(lead + (nq, vd), dtype=dtype, device=x_q.device)
+    o_view = torch.as_strided(o, (batch, h, nq, dv), (nq * vd, dv, vd, 1))
+    ops.attention(q4, k4, v4, None, bias, out=o_view, scale=module.q_scale)
+    ops.linear(xq, nh.linear_weight(module, "gating_query", dtype), None, dtype, out=o,
+               epilogue=nh.EPI_SIGMOID_MUL_AUX, aux=o)
+    return _ada_ln_zero(module.adaptive_zero_init, o, single_cond_q, dtype, accumulate_into)
+
+
+class CrossAttention(nn.Module):
+    def __init__(self, key_dim: int = 128, value_dim: int = 128, c_single_cond: int = 128,
+                 num_head: int = 4) -> None:
+        super().__init__()
+        self.key_dim = key_dim
+        self.value_dim = value_dim
+        self.c_single_cond = c_single_cond
+        self.num_head = num_head
+        self.key_dim_per_head = key_dim // num_head
+        self.value_dim_per_head = value_dim // num_head
+        self.q_scale = self.key_dim_per_head ** (-0.5)
+        self.q_adaptive_layernorm = AdaptiveLayerNorm(key_dim, c_single_cond, use_single_cond=True)
+        self.k_adaptive_layernorm = AdaptiveLayerNorm(key_dim, c_single_cond, use_single_cond=True)
+        self.q_projection = nn.Linear(key_dim, key_dim, bias=True)
+        self.k_projection = nn.Linear(key_dim, key_dim, bias=False)
+        self.v_projection = nn.Linear(value_dim, value_dim, bias=False)
+        self.gating_query = nn.Linear(key_dim, value_dim, bias=False)
+        self.adaptive_zero_init = AdaLNZero(value_dim, value_dim, key_dim, use_single_cond=True)
+
+    def forward(self, x_q, x_k, mask_q, mask_k, pair_logits=None, single_cond_q=None, single_cond_k=None):
+        _require(fastnn_config.dot_product_attention_implementation, "dot_product_attention_implementation")
+        return cross_attention_hip(self, x_q, x_k, mask_q, mask_k, pair_logits, single_cond_q, single_cond_k)
 
 
 class DiffusionTransformer(nn.Module):
