@@ -264,6 +264,12 @@ int xfh_cross_attention_bias(const void *pair_logits, int logits_dtype, const in
                              const void *mask_q, int mask_q_dtype, const void *mask_k, int mask_k_dtype,
                              int64_t batch, int64_t heads, int64_t nq, int64_t nk, float *out, void *stream);
 
+/* y[i] = x[i] converted between f32 and bf16 (round to nearest even), both contiguous with n
+ * elements. The activation cast that torch autocast inserts in front of each Linear
+ * (xfold/fastnn/native.py:31-43 computes in the autocast dtype); the hip modules run it here
+ * instead of in a torch kernel. */
+int xfh_convert(const void *x, int x_dtype, void *y, int y_dtype, int64_t n, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -20,7 +20,7 @@ def dot_product_attention_hip(q, k, v, mask=None, bias=None):
     dtype = nh.compute_dtype(q, k, v)
     if mask is not None and mask.dim() not in (1, 2) and mask.dtype != torch.bool:
         raise ValueError("Attention masks of rank 0/3/4 must be boolean, as in the PyTorch path.")
-    q, k, v = (t if t.dtype == dtype else t.to(dtype) for t in (q, k, v))
+    q, k, v = (t if t.dtype == dtype else ops.as_dtype(t, dtype) for t in (q, k, v))
     return ops.attention(q, k, v, mask, bias)
 
 

@@ -73,6 +73,7 @@ SIGNATURES = {
     "xfh_msa_attention": (_i, [_p, _i, _p, _i, _p, _i, _i64, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p, _f,
                                _p, _p, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
     "xfh_cross_attention_bias": (_i, [_p, _i, _pi64, _p, _i, _p, _i, _i64, _i64, _i64, _i64, _p, _p]),
+    "xfh_convert": (_i, [_p, _i, _p, _i, _i64, _p]),
 }
 
 

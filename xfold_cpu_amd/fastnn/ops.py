@@ -73,6 +73,19 @@ def adaptive_layer_norm(x: torch.Tensor, scale: torch.Tensor, shift: torch.Tenso
     return y
 
 
+def as_dtype(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """x contiguous in ``dtype`` (f32/bf16); a dtype change runs in this library's kernel."""
+    if x.dtype == dtype:
+        return x.contiguous()
+    if x.dtype not in (torch.float32, torch.bfloat16) or dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"as_dtype: {x.dtype} -> {dtype} (f32/bf16 only)")
+    x_c = x.contiguous()
+    y = torch.empty(x.shape, dtype=dtype, device=x.device)
+    nh.call("xfh_convert", nh.ptr(x_c), nh.dtype_code(x.dtype), nh.ptr(y), nh.dtype_code(dtype), x_c.numel(),
+            nh.stream_of(x.device))
+    return y
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], dtype: torch.dtype,
            out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
            epilogue: int = nh.EPI_STORE, aux: Optional[torch.Tensor] = None,
@@ -86,7 +99,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], 
     n = weight.shape[0]
     if weight.shape[1] != k:
         raise ValueError(f"linear: weight {tuple(weight.shape)} does not match input dim {k}")
-    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    x_c = as_dtype(x, dtype)
     m = x_c.numel() // k if k else 0
     if out is None:
         out = torch.empty((*x.shape[:-1], n), dtype=out_dtype or dtype, device=x.device)
@@ -112,7 +125,7 @@ def linear_batched(x: torch.Tensor, weights: torch.Tensor, bias: Optional[torch.
     shared = x.dim() == 2
     if not shared and (x.dim() != 3 or x.shape[0] != nb):
         raise ValueError("linear_batched: x must be [m, k] or [B, m, k]")
-    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    x_c = as_dtype(x, dtype)
     m = x_c.shape[-2]
     out = torch.empty((nb, m, n), dtype=out_dtype or dtype, device=x.device)
     b = None
@@ -130,7 +143,7 @@ def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torc
                       out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """silu(x @ Wg) * (x @ Wv) from the packed weight (``xfold/fastnn/gated_linear_unit.py:103-107``)."""
     k = x.shape[-1]
-    x_c = x if (x.dtype == dtype and x.is_contiguous()) else x.to(dtype).contiguous()
+    x_c = as_dtype(x, dtype)
     m = x_c.numel() // k if k else 0
     y = torch.empty((*x.shape[:-1], f), dtype=out_dtype or dtype, device=x.device)
     nh.call("xfh_gated_linear_unit", nh.ptr(x_c), nh.ptr(packed), m, k, f, nh.dtype_code(dtype),
