@@ -1,13 +1,20 @@
 """Per-kernel rates of the hot operators on one GPU, against MI355X peaks (HBM 8 TB/s, bf16
 dense MFMA 2.5 PFLOP/s).
 
-    python -m xfold_cpu_amd.kernel_bench [--n 768] [--reps 20]
+    python -m xfold_cpu_amd.kernel_bench [--n 768] [--reps 20] [--vendor]
 
 Each operator runs on synthetic bf16 inputs of the Pairformer shapes (pair [N, N, 128]) with
 the library's own HIP-event timing (``xfh_set_kernel_timing``) on, so every figure is the
 average duration of that kernel's launches on its stream. Bytes are the algorithmic HBM bytes
 of one launch (each input read once, each output written once); FLOPs count multiply-adds
 as two. One JSON line per kernel.
+
+``--vendor`` adds reference points from the ROCm libraries behind torch at the same shapes,
+timed with HIP events around the call: hipBLASLt's batched GEMM on the triangle
+contraction's 128 per-channel products, torch's ``scaled_dot_product_attention`` on the
+triangle attention's shape with and without its additive bias, and a square 8192^3 bf16
+GEMM (what a library GEMM reaches of the MFMA peak on this device). They are comparisons,
+not part of the backend.
 """
 
 from __future__ import annotations
@@ -86,10 +93,52 @@ def _line(kernel, workload, ms, launches, gbytes=None, gflop=None):
     print(json.dumps(rec), flush=True)
 
 
+def _event_ms(fn, reps):
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def vendor_points(n: int, reps: int, dev: torch.device, c: int = 128, heads: int = 4, d: int = 32):
+    """Library kernels at this path's shapes (comparisons only)."""
+    g = torch.Generator(device=dev).manual_seed(0)
+    left = torch.randn(c, n, n, device=dev, generator=g).bfloat16()
+    right_t = torch.randn(c, n, n, device=dev, generator=g).bfloat16()      # [k][j]: contiguous operand
+    prod = torch.empty(c, n, n, device=dev, dtype=torch.bfloat16)
+    ms = _event_ms(lambda: torch.bmm(left, right_t, out=prod), reps)
+    _line("vendor: torch.bmm (hipBLASLt)", f"{c} products {n}^3 bf16 (the triangle contraction)", ms, reps,
+          gflop=2 * c * n ** 3 / 1e9)
+    del left, right_t, prod
+    q, k, v = (torch.randn(n, heads, n, d, device=dev, generator=g).bfloat16() for _ in range(3))
+    bias = torch.randn(1, heads, n, n, device=dev, generator=g).bfloat16().expand(n, heads, n, n)
+    flop = 4 * n * heads * n * n * d / 1e9
+    sdpa = torch.nn.functional.scaled_dot_product_attention
+    ms = _event_ms(lambda: sdpa(q, k, v, attn_mask=bias), reps)
+    _line("vendor: scaled_dot_product_attention + bias", f"B={n} H={heads} Q=K={n} D={d} bf16", ms, reps, gflop=flop)
+    ms = _event_ms(lambda: sdpa(q, k, v), reps)
+    _line("vendor: scaled_dot_product_attention", f"B={n} H={heads} Q=K={n} D={d} bf16, no bias", ms, reps,
+          gflop=flop)
+    del q, k, v, bias
+    big = 8192
+    a = torch.randn(big, big, device=dev, generator=g).bfloat16()
+    b = torch.randn(big, big, device=dev, generator=g).bfloat16()
+    out = torch.empty(big, big, device=dev, dtype=torch.bfloat16)
+    ms = _event_ms(lambda: torch.mm(a, b, out=out), max(reps // 2, 3))
+    _line("vendor: torch.mm (hipBLASLt)", f"{big}^3 bf16", ms, reps, gflop=2 * big ** 3 / 1e9)
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     p.add_argument("--n", type=int, default=768)
     p.add_argument("--reps", type=int, default=20)
+    p.add_argument("--vendor", action="store_true", help="add the library reference points")
     args = p.parse_args(argv)
     n, c = args.n, 128
     dev = torch.device("cuda:0")
@@ -133,6 +182,10 @@ def main(argv=None):
             wl = (torch.randn(16, c, device=dev) / c ** 0.5).bfloat16()
             r = _timed(["pair_bias"], lambda: ops.pair_attention_bias(pair, w, b, 1e-5, wl), args.reps)
             _line("pair_bias_kernel", f"pair logits N={n}, 16 heads", *r["pair_bias"], *work["pair_bias"][1:])
+    if args.vendor:
+        del pair, mask
+        with torch.inference_mode():
+            vendor_points(n, args.reps, dev)
 
 
 if __name__ == "__main__":
