@@ -548,3 +548,35 @@ def test_gemm_ring_configurations(device, kind, m, k, n, batch, config):
     # bf16 operands are exact in the fp32 reference: only accumulation order and the bf16
     # store differ, so the floor is the exact result stored in bf16.
     assert_parity_bf16(got, want, f"gemm_ring {config} {kind} {m}x{k}->{n}", floor=bf16_stored(want))
+
+
+@pytest.mark.parametrize("profile", ["jump", "low", "ramp", "mixed"])
+@pytest.mark.parametrize("batch", [3, 8])
+def test_attention_logit_ranges(device, profile, batch):
+    """The pipelined kernel's lazy running maximum (it rescales only when a row's maximum
+    grows by more than a slack) across logit ranges (bias in natural units, fp32): 'jump'
+    lifts the second half of the keys by 150, so every row rescales once mid-row; 'low'
+    puts every logit near -300; 'ramp' raises the logits by up to 200 across the keys,
+    block after block; 'mixed' gives each query its own offset in [-250, 250].
+    Random key masks, 3 (a partial row group) or 8 batch rows, bf16 q/k/v."""
+    announce("attention logit ranges", profile, batch)
+    g = torch.Generator().manual_seed(batch)
+    h, n, d = 4, 200, 32
+    q, k, v = (torch.randn(batch, h, n, d, generator=g).bfloat16() for _ in range(3))
+    bias = torch.randn(h, n, n, generator=g)
+    if profile == "jump":
+        bias[..., n // 2:] += 150.0
+    elif profile == "low":
+        bias -= 300.0
+    elif profile == "ramp":
+        bias += torch.linspace(-100.0, 200.0, n)
+    else:
+        bias += (torch.rand(1, n, 1, generator=g) - 0.5) * 500.0
+    mask = torch.rand(batch, n, generator=g) > 0.2
+    mask[:, 0] = True
+    args = (q.float(), k.float(), v.float(), mask, bias)
+    want = R.dot_product_attention(*args)
+    floor = floor_of(lambda: R.dot_product_attention(*args), stored=True)
+    got = ops.attention(q.to(device), k.to(device), v.to(device), mask.to(device), bias.to(device))
+    assert torch.isfinite(got.float()).all()
+    assert_parity_bf16(got, want, f"attention logits {profile}", floor=floor)
