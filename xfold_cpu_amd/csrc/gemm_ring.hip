@@ -67,13 +67,98 @@ template <> struct Vec4<float> {
   }
 };
 
-__device__ __forceinline__ float epilogue(int epi, float acc, float c, float aux) {
-  switch (epi) {
-    case XFH_EPI_MUL_SIGMOID_AUX: return acc * sigmoidf_(aux);
-    case XFH_EPI_SIGMOID_MUL_AUX: return sigmoidf_(acc) * aux;
-    case XFH_EPI_ACCUMULATE: return c + acc;
-    case XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE: return c + acc * sigmoidf_(aux);
-    default: return acc;
+template <int EPI> __device__ __forceinline__ float epilogue(float acc, float c, float aux) {
+  if constexpr (EPI == XFH_EPI_MUL_SIGMOID_AUX) return acc * sigmoidf_(aux);
+  else if constexpr (EPI == XFH_EPI_SIGMOID_MUL_AUX) return sigmoidf_(acc) * aux;
+  else if constexpr (EPI == XFH_EPI_ACCUMULATE) return c + acc;
+  else if constexpr (EPI == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE) return c + acc * sigmoidf_(aux);
+  else return acc;
+}
+
+// Stores one wavefront's 64 x (16 NT) sub-tile (rows mw + 16 y + col, columns nw + 16 x +
+// 4 grp + e) through epilogue EPI. The epilogue kind is a template parameter and the row
+// quantities (row divisor, auxiliary row) are taken once per row: a runtime switch per
+// element made this code ~10x larger than the main loop, and its instruction-cache misses
+// cost ~10 us per launch whatever the grid.
+template <int EPI, typename TO, int NT>
+__device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)[NT][4], int64_t batch, int mw,
+                                           int nw, int col, int grp) {
+  constexpr bool READS_C = EPI == XFH_EPI_ACCUMULATE || EPI == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
+  constexpr bool AUX = EPI == XFH_EPI_MUL_SIGMOID_AUX || EPI == XFH_EPI_SIGMOID_MUL_AUX ||
+                       EPI == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
+  TO *C = static_cast<TO *>(p.C) + batch * p.sC;
+  int m[4];
+  float rs[4];
+  const TO *arow[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    m[y] = mw + y * 16 + col;
+    rs[y] = p.row_div && m[y] < p.M ? 1.0f / (p.row_div_eps + p.row_div[m[y]]) : 1.0f;
+    arow[y] = nullptr;
+    if constexpr (AUX) {
+      const int ar = p.aux_rows > 0 ? m[y] % int(p.aux_rows) : m[y];
+      arow[y] = static_cast<const TO *>(p.aux) + batch * p.sAux + int64_t(ar) * p.ldaux;
+    }
+  }
+  if (p.pair_blk == 0 && mw + 64 <= p.M && nw + 16 * NT <= p.N) {
+    // Interior sub-tile (every tile of the usual shapes): straight-line code, no per-element
+    // bounds, row-major addresses.
+#pragma unroll
+    for (int x = 0; x < NT; ++x) {
+      const int n = nw + x * 16 + grp * 4;
+      float bias[4] = {0.f, 0.f, 0.f, 0.f};
+      if (p.bias)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) bias[e] = p.bias[batch * p.sBias + n + e];
+#pragma unroll
+      for (int y = 0; y < 4; ++y) {
+        TO *c = C + int64_t(m[y]) * p.ldc + n;
+        float cv[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f}, out[4];
+        if constexpr (READS_C) Vec4<TO>::load(c, cv);
+        if constexpr (AUX) Vec4<TO>::load(arow[y] + n, av);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) out[e] = epilogue<EPI>((acc[x][y][e] + bias[e]) * rs[y], cv[e], av[e]);
+        Vec4<TO>::store(c, out);
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int x = 0; x < NT; ++x) {
+    const int n = nw + x * 16 + grp * 4;
+    if (n >= p.N) continue;
+    const bool full = n + 4 <= p.N;
+    float bias[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias[e] = n + e < p.N ? p.bias[batch * p.sBias + n + e] : 0.f;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      if (m[y] >= p.M) continue;
+      TO *c = c_element(p, C, m[y], n);
+      float cv[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f}, out[4];
+      if (full) {
+        if constexpr (READS_C) Vec4<TO>::load(c, cv);
+        if constexpr (AUX) Vec4<TO>::load(arow[y] + n, av);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if (n + e >= p.N) continue;
+          if constexpr (READS_C) cv[e] = to_f32(c[e]);
+          if constexpr (AUX) av[e] = to_f32(arow[y][n + e]);
+        }
+      }
+      // (acc + bias) * 1.0f is exact, so rows without a divisor keep acc + bias.
+#pragma unroll
+      for (int e = 0; e < 4; ++e) out[e] = epilogue<EPI>((acc[x][y][e] + bias[e]) * rs[y], cv[e], av[e]);
+      if (full) {
+        Vec4<TO>::store(c, out);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (n + e < p.N) c[e] = from_f32<TO>(out[e]);
+      }
+    }
   }
 }
 
@@ -94,16 +179,22 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
   __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * G::SLOT_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
-  // Tiles are numbered row-major (the n tiles of one row block consecutive). With XCD each
-  // XCD (workgroups are dealt round-robin to the 8 XCDs) takes a contiguous run of them,
-  // so a row block of A is fetched into one XCD's L2 rather than into all eight.
+  // With XCD the grid is 1-D and workgroup i runs on XCD i % 8 (workgroups are dealt
+  // round-robin to the 8 XCDs). The output's tiles are split into 8 / g row groups times g
+  // column groups (g = xcd_split); XCD x takes rectangle x, row-major inside it, so each
+  // XCD's L2 holds the A row blocks and B column tiles of one rectangle rather than a
+  // scatter over all of them. Workgroups past a rectangle's edge exit at once.
   int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
-  if constexpr (XCD) {                              // 1-D grid, remapped
-    const int ntiles = (p.N + BN - 1) / BN, tiles = ntiles * ((p.M + BM - 1) / BM);
-    const int logical = int(blockIdx.x % 8) * int(gridDim.x / 8) + int(blockIdx.x / 8);
-    if (logical >= tiles) return;
-    m0 = (logical / ntiles) * BM;
-    n0 = (logical % ntiles) * BN;
+  if constexpr (XCD) {
+    const int tn = (p.N + BN - 1) / BN, tm = (p.M + BM - 1) / BM;
+    const int gn = p.xcd_split, gm = 8 / gn;
+    const int cn = (tn + gn - 1) / gn, cm = (tm + gm - 1) / gm;
+    const int xcd = int(blockIdx.x % 8), local = int(blockIdx.x / 8);
+    const int n_lo = (xcd % gn) * cn, m_lo = (xcd / gn) * cm;
+    const int w = min(cn, tn - n_lo), h = min(cm, tm - m_lo);
+    if (w <= 0 || h <= 0 || local >= w * h) return;
+    m0 = (m_lo + local / w) * BM;
+    n0 = (n_lo + local % w) * BN;
   }
   const int64_t batch = blockIdx.z;
   const bf16 *A = static_cast<const bf16 *>(p.A) + batch * p.sA;
@@ -200,50 +291,22 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     }
     return;
   }
-  const TO *aux = static_cast<const TO *>(p.aux);
-#pragma unroll
-  for (int x = 0; x < NT; ++x) {
-    const int n = n0 + wn * WN + x * 16 + grp * 4;
-    if (n >= p.N) continue;
-    const bool full = n + 4 <= p.N;
-    float bias[4] = {0.f, 0.f, 0.f, 0.f};
-    if (p.bias)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) bias[e] = n + e < p.N ? p.bias[batch * p.sBias + n + e] : 0.f;
-#pragma unroll
-    for (int y = 0; y < 4; ++y) {
-      const int m = m0 + wm * 64 + y * 16 + col;
-      if (m >= p.M) continue;
-      TO *c = c_element(p, C, m, n);
-      const TO *a = nullptr;
-      if (aux) {
-        const int64_t ar = p.aux_rows > 0 ? (m % p.aux_rows) : m;
-        a = aux + batch * p.sAux + ar * p.ldaux + n;
-      }
-      const bool reads_c = p.epi == XFH_EPI_ACCUMULATE || p.epi == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
-      float cv[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f}, out[4];
-      if (full) {
-        if (reads_c) Vec4<TO>::load(c, cv);
-        if (a) Vec4<TO>::load(a, av);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          if (n + e >= p.N) continue;
-          if (reads_c) cv[e] = to_f32(c[e]);
-          if (a) av[e] = to_f32(a[e]);
-        }
-      }
-      const float rs = p.row_div ? 1.0f / (p.row_div_eps + p.row_div[m]) : 1.0f;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) out[e] = epilogue(p.epi, p.row_div ? (acc[x][y][e] + bias[e]) * rs : acc[x][y][e] + bias[e], cv[e], av[e]);
-      if (full) {
-        Vec4<TO>::store(c, out);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (n + e < p.N) c[e] = from_f32<TO>(out[e]);
-      }
-    }
+  const int mw = m0 + wm * 64, nw = n0 + wn * WN;
+  switch (p.epi) {
+    case XFH_EPI_MUL_SIGMOID_AUX:
+      store_tile<XFH_EPI_MUL_SIGMOID_AUX, TO, NT>(p, acc, batch, mw, nw, col, grp);
+      break;
+    case XFH_EPI_SIGMOID_MUL_AUX:
+      store_tile<XFH_EPI_SIGMOID_MUL_AUX, TO, NT>(p, acc, batch, mw, nw, col, grp);
+      break;
+    case XFH_EPI_ACCUMULATE:
+      store_tile<XFH_EPI_ACCUMULATE, TO, NT>(p, acc, batch, mw, nw, col, grp);
+      break;
+    case XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE:
+      store_tile<XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE, TO, NT>(p, acc, batch, mw, nw, col, grp);
+      break;
+    default:
+      store_tile<XFH_EPI_STORE, TO, NT>(p, acc, batch, mw, nw, col, grp);
   }
 }
 
@@ -261,16 +324,25 @@ using RingXWide = Ring<192, 64, 2, 2>;     // 1.5x-width tiles: one round where 
 template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
   const int64_t tiles = ceil_div(p.N, G::BN) * ceil_div(p.M, G::BM);
   if (tiles > (int64_t(1) << 30)) return fail(XFH_EUNSUPPORTED, "gemm_ring: too many tiles");
-  const dim3 grid = p.xcd_rows ? dim3(unsigned(ceil_div(tiles, 8) * 8), 1, unsigned(batch))
-                               : dim3(unsigned(ceil_div(p.N, G::BN)), unsigned(ceil_div(p.M, G::BM)), unsigned(batch));
+  dim3 grid(unsigned(ceil_div(p.N, G::BN)), unsigned(ceil_div(p.M, G::BM)), unsigned(batch));
+  if (p.xcd_split) {
+    const int64_t gn = p.xcd_split, gm = 8 / gn;
+    grid = dim3(unsigned(8 * ceil_div(ceil_div(p.N, G::BN), gn) * ceil_div(ceil_div(p.M, G::BM), gm)), 1,
+                unsigned(batch));
+  }
   if (glu) {
     if constexpr (G::NT % 2 == 0) {
-      if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G><<<grid, 256, 0, s>>>(p);
-      else gemm_ring_kernel<float, true, G><<<grid, 256, 0, s>>>(p);
+      if (p.xcd_split) {
+        if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G, true><<<grid, 256, 0, s>>>(p);
+        else gemm_ring_kernel<float, true, G, true><<<grid, 256, 0, s>>>(p);
+      } else {
+        if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G><<<grid, 256, 0, s>>>(p);
+        else gemm_ring_kernel<float, true, G><<<grid, 256, 0, s>>>(p);
+      }
     } else {
       return fail(XFH_EUNSUPPORTED, "gemm_ring: GLU needs whole 32-column groups per wavefront");
     }
-  } else if (p.xcd_rows) {
+  } else if (p.xcd_split) {
     if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, false, G, true><<<grid, 256, 0, s>>>(p);
     else gemm_ring_kernel<float, false, G, true><<<grid, 256, 0, s>>>(p);
   } else {
@@ -311,7 +383,7 @@ bool gemm_ring_supported(const GemmArgs &p, int out_dtype) {
   if (p.pair_blk && (p.pair_blk % 4 || !aligned(p.C, 4 * ob) || p.sC % 4)) return false;
   const bool vec_out = p.ldc % 4 == 0 && p.sC % 4 == 0 && aligned(p.C, 4 * ob) &&
                        (!p.aux || (p.ldaux % 4 == 0 && p.sAux % 4 == 0 && aligned(p.aux, 4 * ob)));
-  return p.K > 0 && p.K % 32 == 0 && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sA % 8 == 0 &&
+  return p.K > 0 && p.K % 32 == 0 && p.aux_rows <= INT32_MAX && p.lda % 8 == 0 && p.ldb % 8 == 0 && p.sA % 8 == 0 &&
          p.sB % 8 == 0 && aligned(p.A, 16) && aligned(p.B, 16) && vec_out;
 }
 
@@ -325,15 +397,15 @@ int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStre
   // in one XCD's 4 MB L2 and the grid covers every CU (measured: 8% on 3840 x 768 outputs;
   // slower when B crowds the L2 or a row block is one tile).
   GemmArgs q = p;
-  q.xcd_rows = !glu && p.K % 64 == 0 && int64_t(p.N) * p.K * 2 <= (int64_t(5) << 19) && p.N > bn &&
-               ceil_div(p.M, 128) * ceil_div(p.N, bn) >= cus;
+  q.xcd_split = (!glu && p.K % 64 == 0 && int64_t(p.N) * p.K * 2 <= (int64_t(5) << 19) && p.N > bn &&
+                 ceil_div(p.M, 128) * ceil_div(p.N, bn) >= cus) ? 1 : 0;
   // The configuration is observable through the kernel timer of that name.
   static const char *const names[5][2] = {{"gemm_ring.mid", "gemm_ring.mid+xcd"},
                                           {"gemm_ring.narrow", "gemm_ring.narrow+xcd"},
                                           {"gemm_ring.shallow", "gemm_ring.shallow+xcd"},
                                           {"gemm_ring.shallow_narrow", "gemm_ring.shallow_narrow+xcd"},
                                           {"gemm_ring.xwide", "gemm_ring.xwide+xcd"}};
-  KernelTimer config_timer(names[int(pick)][q.xcd_rows ? 1 : 0], s);
+  KernelTimer config_timer(names[int(pick)][q.xcd_split ? 1 : 0], s);
   switch (pick) {
     case RingPick::Mid: return launch_ring<RingMid>(q, batch, out_dtype, glu, s);
     case RingPick::XWide: return launch_ring<RingXWide>(q, batch, out_dtype, glu, s);

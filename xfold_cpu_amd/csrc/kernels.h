@@ -18,7 +18,9 @@ struct GemmArgs {
   int64_t ldaux, sAux, aux_rows;
   int M, N, K;
   int epi;                  // XFH_EPI_*
-  int xcd_rows;             // gemm_ring: give each XCD a contiguous run of row-major tiles
+  // gemm_ring tile placement: 0 = plain 2-D grid; g in {1, 2, 4, 8} = each XCD takes one
+  // rectangle of tiles out of a (8/g row groups) x (g column groups) split of the output.
+  int xcd_split;
   int glu_f;                // GLU output features (GLU launches only)
   // Row divisor: the value (acc + bias) of row m is divided by (row_div_eps + row_div[m])
   // before the epilogue (fp32 [M], null = none).
