@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 7
+#define XFH_ABI_VERSION 8
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -147,6 +147,46 @@ int64_t xfh_attention_max_keys(void);
  * instead of once per block. */
 int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides,
                             void *packed, void *stream);
+
+/* Self-attention on operands in the pipelined attention kernel's own layouts, for B
+ * samples of T tokens and H heads of Dh (Dh a multiple of 4, at most 64; T at most
+ * xfh_attention_max_keys()): Dp = 32 (Dh <= 32) or 64, Tpad = align64(T), and bf16
+ *   q [B][H][T][Dp], k [B][H][Tpad][Dp], vt [B][H][Dp][Tpad] (keys permuted inside runs of 32).
+ * The three calls below split SelfAttention.forward (xfold/nn/diffusion_transformer.py:
+ * 184-217: q/k/v projections, dot_product_attention, gating) so that the projection GEMM
+ * writes these layouts directly and the gate is applied at the attention's store, with no
+ * layout conversion in between; xfh_dot_product_attention keeps the general contract.
+ * sizes[0..4] = {Dp, Tpad, q elements, k elements, vt elements}; XFH_EUNSUPPORTED for other
+ * head dims or token counts. */
+int xfh_attention_operands_size(int64_t B, int64_t T, int64_t H, int64_t Dh, int64_t *sizes);
+
+/* [q | k | v (| gate)] = x w^T + bias in one bf16 GEMM, straight into those layouts:
+ * x [B*T][K] bf16 (row stride ldx), w [N][K] bf16 = the stacked projection weights
+ * [Wq; Wk; Wv] (N = 3c, c = H*Dh) or [Wq; Wk; Wv; Wg] (N = 4c, gate != NULL), bias fp32
+ * [N] or NULL. q is multiplied by qscale; gate [B][T][c] bf16 holds the gating Linear's
+ * output (before its sigmoid). The padding of q, k and vt (head dims >= Dh, keys >= T) is
+ * never written: allocate them zeroed once and reuse them. Needs K % 32 == 0, ldx % 8 == 0
+ * and 16-byte aligned x and w (XFH_EUNSUPPORTED otherwise). */
+int xfh_attention_project(const void *x, int64_t ldx, const void *w, const float *bias, int64_t B, int64_t T,
+                          int64_t K, int64_t H, int64_t Dh, float qscale, void *q, void *k, void *vt, void *gate,
+                          void *stream);
+
+/* Kept-key words of a key mask for xfh_attention_operands: words[b][w] bit j is set iff key
+ * 64w + j < T is kept, i.e. mask[b*mask_stride + key] != 0 (NaN kept, as the reference's
+ * .to(bool)); mask NULL keeps every key. words holds rows * align64(T)/64 uint64. */
+int xfh_attention_mask_words(const void *mask, int mask_dtype, int64_t mask_stride, int64_t rows, int64_t T,
+                             uint64_t *words, void *stream);
+
+/* out [B][T][H*Dh] bf16 = softmax(q k^T + bias, masked keys removed) v over operands written
+ * by xfh_attention_project (q already scaled), times sigmoid(gate) elementwise when gate is
+ * given (gate [B][T][H*Dh] bf16: SelfAttention's gating, diffusion_transformer.py:209-211).
+ * bias = one packed [H][T][Tpad] block (xfh_attention_bias_pack, xfh_pair_attention_bias),
+ * required; words from xfh_attention_mask_words with rows = B, or rows = 1 and
+ * words_shared = 1 for a mask shared by the samples. A row whose keys are all masked
+ * averages v uniformly, as the reference's -1e9 fill does. */
+int xfh_attention_operands(const void *q, const void *k, const void *vt, const uint64_t *words, int words_shared,
+                           const float *bias, const void *gate, void *out, int64_t B, int64_t T, int64_t H,
+                           int64_t Dh, void *stream);
 
 /* Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' straight into the packed bias layout
  * of xfh_attention_bias_pack: packed[h][i][j] fp32 = log2(e) * (LN(pair[i][j]) . w[h]) for

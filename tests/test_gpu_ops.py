@@ -476,6 +476,102 @@ def test_self_attention(device, cond, bf16):
                  "self attention")
 
 
+@pytest.mark.parametrize("c,heads,samples,n,mask_kind", [
+    (768, 16, 5, 200, "tail"),          # the diffusion transformer's heads (Dh 48)
+    (384, 16, 1, 77, "tail"),           # the Pairformer single track (Dh 24), ragged T
+    (256, 4, 3, 130, "per_sample"),     # Dh 64, a different key mask per sample
+    (128, 4, 2, 64, "none"),            # Dh 32, no mask
+    (768, 16, 2, 40, "one_row_empty"),  # sample 1 keeps no key: uniform average of v
+])
+def test_self_attention_operand_path(device, monkeypatch, c, heads, samples, n, mask_kind):
+    """bf16 SelfAttention with a packed bias: one GEMM writes q (pre-scaled), k, v^T and the
+    gate straight into the attention kernel's layouts and the gate is applied at the
+    attention's store. The general attention entry must not be called."""
+    announce("self_attention operand path", c, heads, samples, n, mask_kind)
+    monkeypatch.setattr(ops, "attention", lambda *a, **k: pytest.fail("general attention path taken"))
+    ref, hip = pair_of("SelfAttention", dict(c_x=c, c_single_cond=64, num_head=heads, use_single_cond=True),
+                       seed=c + n)
+    g = torch.Generator().manual_seed(n)
+    x = torch.randn(samples, n, c, generator=g).bfloat16()
+    logits = torch.randn(heads, n, n, generator=g)
+    single = torch.randn(n, 64, generator=g)
+    if mask_kind == "none":
+        mask, rows = None, [None] * samples
+    elif mask_kind == "tail":
+        mask = torch.ones(n)
+        mask[-5:] = 0
+        rows = [mask] * samples
+    else:
+        mask = (torch.rand(samples, n, generator=g) > 0.3).float()
+        mask[:, 0] = 1
+        if mask_kind == "one_row_empty":
+            mask[1] = 0
+        rows = list(mask)
+
+    def oracle():
+        return torch.stack([ref(x[s].float(), rows[s], logits, single) for s in range(samples)])
+    dev_mask = None if mask is None else mask.to(device)
+    with torch.inference_mode():
+        want = oracle()
+        packed = ops.PackedBias(ops.attention_bias_pack(logits[None].to(device))[0])
+        with autocast(True):
+            got = hnn.self_attention_hip(hip, x.to(device), dev_mask, packed, single.to(device))
+    assert_parity_bf16(got, want, "self attention operand path", floor=bf16_stored(floor_of(oracle)))
+
+
+def test_attention_operands_reused(device):
+    """One AttentionOperands set reused over calls with different inputs gives the same bits
+    as a fresh set: the projection never writes the zero padding the kernel reads."""
+    announce("attention operands reused")
+    _, hip = pair_of("SelfAttention", dict(c_x=384, c_single_cond=64, num_head=16, use_single_cond=True), seed=3)
+    hip = hip.to(device)
+    g = torch.Generator().manual_seed(3)
+    n = 70
+    xs = [torch.randn(2, n, 384, generator=g).bfloat16().to(device) for _ in range(2)]
+    mask = torch.ones(n, device=device)
+    mask[-3:] = 0
+    packed = ops.PackedBias(ops.attention_bias_pack(torch.randn(1, 16, n, n, generator=g).to(device))[0])
+    single = torch.randn(n, 64, generator=g).to(device)
+    shared = ops.AttentionOperands(2, n, 16, 24, device)
+    with torch.inference_mode(), autocast(True):
+        outs = [hnn.self_attention_hip(hip, x, mask, packed, single, _operands=shared) for x in xs]
+        fresh = hnn.self_attention_hip(hip, xs[1], mask, packed, single)
+    assert torch.equal(outs[1], fresh)
+    assert not torch.equal(outs[0], outs[1])
+    # The padding of q (head dims 24..31), k (keys >= 70) and v^T is still zero.
+    q = shared.q.view(2, 16, n, shared.dp)
+    assert q[..., 24:].abs().max().item() == 0
+    k = shared.k.view(2, 16, shared.tpad, shared.dp)
+    assert k[:, :, n:].abs().max().item() == 0 and k[..., 24:].abs().max().item() == 0
+    vt = shared.vt.view(2, 16, shared.dp, shared.tpad)
+    assert vt[:, :, 24:].abs().max().item() == 0
+
+
+def test_attention_project_layouts(device):
+    """xfh_attention_project's layouts against the stacked projection computed by a plain
+    GEMM: q = (x Wq^T + b) * qscale, k, v^T (keys permuted inside runs of 32) and the gate,
+    at the bf16 bar (the layouts hold the bf16-rounded products)."""
+    announce("attention project layouts")
+    B, T, H, Dh, K = 2, 45, 4, 20, 64
+    c = H * Dh
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B * T, K, generator=g).bfloat16().to(device)
+    w = (torch.randn(4 * c, K, generator=g) / 8).bfloat16().to(device)
+    bias = torch.randn(4 * c, generator=g).to(device)
+    ops_ = ops.AttentionOperands(B, T, H, Dh, device)
+    ops.attention_project(x, w, bias, ops_, 0.5)
+    full = x.float() @ w.float().t() + bias                              # [B*T, 4c]
+    parts = full.view(B, T, 4, H, Dh)
+    q = ops_.q.view(B, H, T, ops_.dp)[..., :Dh].float()
+    assert_parity(q, (parts[:, :, 0] * 0.5).permute(0, 2, 1, 3), TOL_BF16, "q layout")
+    k = ops_.k.view(B, H, ops_.tpad, ops_.dp)[:, :, :T, :Dh].float()
+    assert_parity(k, parts[:, :, 1].permute(0, 2, 1, 3), TOL_BF16, "k layout")
+    pos = torch.tensor([(t & ~31) + ((t & 15) >> 2) * 8 + ((t & 31) >> 4) * 4 + (t & 3) for t in range(T)])
+    vt = ops_.vt.view(B, H, ops_.dp, ops_.tpad)[:, :, :Dh].float()[..., pos.to(device)]
+    assert_parity(vt, parts[:, :, 2].permute(0, 2, 3, 1), TOL_BF16, "v^T layout")
+    assert_parity(ops_.gate.float(), parts[:, :, 3].reshape(B, T, c), TOL_BF16, "gate layout")
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_diffusion_transition(device, bf16):
     announce("diffusion_transition", bf16)

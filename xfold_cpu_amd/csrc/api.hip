@@ -343,6 +343,69 @@ int xfh_attention_bias_pack(const void *bias, int dtype, const int64_t *shape, c
   return attention_bias_pack(bias, dtype, shape, strides, packed, as_stream(stream));
 }
 
+int xfh_attention_operands_size(int64_t B, int64_t T, int64_t H, int64_t Dh, int64_t *sizes) {
+  XFH_REQUIRE(sizes && B >= 0 && H >= 0, "attention_operands_size: bad arguments");
+  int dp = 0;
+  int64_t tpad = 0;
+  XFH_TRY(attention_operands_dims(T, Dh, &dp, &tpad));
+  sizes[0] = dp;
+  sizes[1] = tpad;
+  sizes[2] = B * H * T * dp;
+  sizes[3] = B * H * tpad * dp;
+  sizes[4] = B * H * dp * tpad;
+  return XFH_OK;
+}
+
+int xfh_attention_project(const void *x, int64_t ldx, const void *w, const float *bias, int64_t B, int64_t T,
+                          int64_t K, int64_t H, int64_t Dh, float qscale, void *q, void *k, void *vt, void *gate,
+                          void *stream) {
+  XFH_REQUIRE(B >= 0 && H > 0 && K > 0 && ldx >= K, "attention_project: bad sizes");
+  int dp = 0;
+  int64_t tpad = 0;
+  XFH_TRY(attention_operands_dims(T, Dh, &dp, &tpad));
+  const int64_t c = H * Dh, n = (gate ? 4 : 3) * c, m = B * T;
+  XFH_REQUIRE(m < (int64_t(1) << 31) && n < (int64_t(1) << 31) && K < (int64_t(1) << 31),
+              "attention_project: sizes must fit in 32 bits");
+  if (m == 0) return XFH_OK;
+  XFH_REQUIRE(x && w && q && k && vt, "attention_project: null tensor");
+  auto al8 = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 8 == 0; };
+  XFH_REQUIRE(al8(q) && al8(k) && al8(vt) && (!gate || al8(gate)), "attention_project: outputs must be 8-byte aligned");
+  GemmArgs g = gemm_args(x, ldx, w, K, q, n, m, n, K);
+  g.bias = bias;
+  g.attn.q = static_cast<bf16 *>(q);
+  g.attn.k = static_cast<bf16 *>(k);
+  g.attn.vt = static_cast<bf16 *>(vt);
+  g.attn.gate = static_cast<bf16 *>(gate);
+  g.attn.T = int(T); g.attn.Tpad = int(tpad); g.attn.H = int(H); g.attn.Dh = int(Dh); g.attn.Dp = dp;
+  g.attn.qscale = qscale;
+  if (!gemm_ring_supported(g, XFH_BF16))
+    return fail(XFH_EUNSUPPORTED, "attention_project: needs K % 32 == 0, ldx % 8 == 0 and 16-byte aligned x and w");
+  return gemm_ring(g, 1, XFH_BF16, false, as_stream(stream));
+}
+
+int xfh_attention_mask_words(const void *mask, int mask_dtype, int64_t mask_stride, int64_t rows, int64_t T,
+                             uint64_t *words, void *stream) {
+  XFH_REQUIRE(rows >= 0 && T >= 0 && mask_stride >= 0, "attention_mask_words: bad sizes");
+  XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "attention_mask_words: bad mask dtype");
+  if (rows * T == 0) return XFH_OK;
+  XFH_REQUIRE(words, "attention_mask_words: null words");
+  return attention_mask_words(mask, mask_dtype, mask_stride, rows, T, words, as_stream(stream));
+}
+
+int xfh_attention_operands(const void *q, const void *k, const void *vt, const uint64_t *words, int words_shared,
+                           const float *bias, const void *gate, void *out, int64_t B, int64_t T, int64_t H,
+                           int64_t Dh, void *stream) {
+  XFH_REQUIRE(B >= 0 && H > 0, "attention_operands: bad sizes");
+  if (B == 0) return XFH_OK;
+  XFH_REQUIRE(q && k && vt && words && bias && out, "attention_operands: null tensor (the bias is required)");
+  XFH_REQUIRE(reinterpret_cast<uintptr_t>(out) % 8 == 0 && (!gate || reinterpret_cast<uintptr_t>(gate) % 8 == 0),
+              "attention_operands: out and gate must be 8-byte aligned");
+  return attention_operands(static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
+                            static_cast<const bf16 *>(vt), words, words_shared != 0, bias,
+                            static_cast<const bf16 *>(gate), static_cast<bf16 *>(out), B, T, H, Dh,
+                            as_stream(stream));
+}
+
 int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t c, const float *ln_w,
                             const float *ln_b, float eps, const void *w, int w_dtype, int64_t heads,
                             void *packed, void *stream) {

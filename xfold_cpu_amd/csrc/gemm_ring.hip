@@ -15,6 +15,8 @@
 // all work on 4-element vectors and the stores are 8 (bf16) or 16 (fp32) bytes.
 // The launcher picks the tile width, depth and ring from the problem's shape (more
 // workgroups for narrow outputs, deeper k-steps when k allows).
+#include <type_traits>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -162,6 +164,60 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)
   }
 }
 
+// Position of key t inside the attention kernel's V^T rows: within each run of 32 keys,
+// key 4g + j goes to 8g + j and key 16 + 4g + j to 8g + 4 + j (g, j < 4).
+__device__ __forceinline__ int vt_position(int t) {
+  const int w = t & 31;
+  return (t & ~31) + ((w & 15) >> 2) * 8 + ((w >> 4) << 2) + (w & 3);
+}
+
+// Store epilogue into the attention-operand layouts (AttnOut): (acc + bias), times qscale
+// for the q columns. Four consecutive columns share one part and head (Dh % 4 == 0): q, k
+// and gate take one 8-byte store, V^T four 2-byte stores (one per head-dim row).
+template <int NT>
+__device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)[NT][4], int mw, int nw, int col,
+                                           int grp) {
+  const AttnOut &o = p.attn;
+  const int c = o.H * o.Dh;
+  int smp[4], tok[4];                                 // per row: sample b and token t
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int m = mw + y * 16 + col;
+    smp[y] = m / o.T;
+    tok[y] = m - smp[y] * o.T;
+  }
+#pragma unroll
+  for (int x = 0; x < NT; ++x) {
+    const int n = nw + x * 16 + grp * 4;
+    if (n >= p.N) continue;
+    const int part = n / c, w = n - part * c, h = w / o.Dh, d = w - h * o.Dh;
+    const float scale = part == 0 ? o.qscale : 1.0f;
+    float bias[4] = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) bias[e] = p.bias[n + e];
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      if (mw + y * 16 + col >= p.M) continue;
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = bf16((acc[x][y][e] + bias[e]) * scale);
+      const int64_t bh = int64_t(smp[y]) * o.H + h;
+      if (part == 0) {
+        *reinterpret_cast<bf16x4 *>(o.q + (bh * o.T + tok[y]) * o.Dp + d) = v;
+      } else if (part == 1) {
+        *reinterpret_cast<bf16x4 *>(o.k + (bh * o.Tpad + tok[y]) * o.Dp + d) = v;
+      } else if (part == 2) {
+        bf16 *dst = o.vt + (bh * o.Dp + d) * o.Tpad + vt_position(tok[y]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dst[int64_t(e) * o.Tpad] = v[e];
+      } else {
+        *reinterpret_cast<bf16x4 *>(o.gate + (int64_t(smp[y]) * o.T + tok[y]) * c + w) = v;
+      }
+    }
+  }
+}
+
 template <class G, int N> __device__ __forceinline__ void wait_younger(int younger) {
   // Waits until at most `younger` k-steps of this wavefront's loads are in flight.
   if constexpr (N == 0) {
@@ -292,6 +348,12 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     return;
   }
   const int mw = m0 + wm * 64, nw = n0 + wn * WN;
+  if constexpr (std::is_same<TO, bf16>::value) {
+    if (p.attn.q) {
+      store_attn<NT>(p, acc, mw, nw, col, grp);
+      return;
+    }
+  }
   switch (p.epi) {
     case XFH_EPI_MUL_SIGMOID_AUX:
       store_tile<XFH_EPI_MUL_SIGMOID_AUX, TO, NT>(p, acc, batch, mw, nw, col, grp);

@@ -455,13 +455,26 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       const float l = __shfl(o[r][tq][DT][0], col, 64);  // denominator sits in lane `col`, grp 0
       if (b >= a.B || q >= a.Nq) continue;
       const float inv = 1.0f / (all_masked[r] ? float(a.N) : l);
-      bf16 *dst = a.out + int64_t(b) * a.osb + int64_t(q) * a.ost + int64_t(h) * a.ohs + grp * 4;
+      const int64_t off = int64_t(b) * a.osb + int64_t(q) * a.ost + int64_t(h) * a.ohs + grp * 4;
+      bf16 *dst = a.out + off;
 #pragma unroll
       for (int t = 0; t < DT; ++t) {
         const int d = t * 16 + grp * 4;
+        float g[4] = {1.f, 1.f, 1.f, 1.f};
+        if (a.gate) {
+          if (d + 4 <= a.Dv) {
+            const bf16x4 gv = *reinterpret_cast<const bf16x4 *>(a.gate + off + t * 16);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) g[e] = sigmoidf_(static_cast<float>(gv[e]));
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (d + e < a.Dv) g[e] = sigmoidf_(static_cast<float>(a.gate[off + t * 16 + e]));
+          }
+        }
         bf16x4 v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = bf16(o[r][tq][t][e] * inv);
+        for (int e = 0; e < 4; ++e) v[e] = bf16(g[e] * (o[r][tq][t][e] * inv));
         if (d + 4 <= a.Dv) {
           *reinterpret_cast<bf16x4 *>(dst + t * 16) = v;
         } else {

@@ -5,6 +5,19 @@
 
 namespace xfh {
 
+// Attention-operand output of a fused [q | k | v | gate] projection (gemm_ring, bf16 out,
+// store epilogue): row m = b*T + t, column n = part*c + h*Dh + d (c = H*Dh) goes to
+//   part 0: q    [B][H][T][Dp]    times qscale
+//   part 1: k    [B][H][Tpad][Dp]
+//   part 2: vt   [B][H][Dp][Tpad] with the attention kernel's key order inside runs of 32
+//   part 3: gate [B][T][c]        (the gating Linear, when N = 4c)
+// The head-dim padding (d >= Dh) and key padding (t >= T) are never written.
+struct AttnOut {
+  bf16 *q, *k, *vt, *gate;   // q null: row-major output
+  int T, Tpad, H, Dh, Dp;
+  float qscale;
+};
+
 struct GemmArgs {
   const void *A;
   int64_t lda, sA;          // row stride, batch stride (elements)
@@ -30,6 +43,7 @@ struct GemmArgs {
   // [M = I*blk] x [N = J*blk] product goes to C[((m/blk * J + n/blk) * blk + m%blk) * blk + n%blk],
   // i.e. the [I][blk] x [J][blk] result stored as [I][J][blk][blk] (ldc unused).
   int pair_blk;
+  AttnOut attn;             // attention-operand layout (attn.q != null), gemm_ring only
 };
 
 // Address of element (m, n) of C (row-major, or the pair-block layout).
@@ -72,6 +86,14 @@ bool mha_supported(const AttentionArgs &a, int dtype);
 int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStream_t s);
 int attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const int64_t *strides, void *packed,
                         hipStream_t s);
+// Self-attention on operands already in the pipelined kernel's layouts (mha.hip): padded
+// head dim and key count, kept-key words, and the attention with an optional gate.
+int attention_operands_dims(int64_t T, int64_t Dh, int *dp, int64_t *tpad);
+int attention_mask_words(const void *mask, int dtype, int64_t stride, int64_t rows, int64_t T, uint64_t *words,
+                         hipStream_t s);
+int attention_operands(const bf16 *q, const bf16 *k, const bf16 *vt, const uint64_t *words, bool words_shared,
+                       const float *bias, const bf16 *gate, bf16 *out, int64_t B, int64_t T, int64_t H, int64_t Dh,
+                       hipStream_t s);
 // Linear(LayerNorm(pair)) straight into the packed attention-bias layout (pair_bias.hip).
 struct PairBiasArgs {
   const void *pair;          // [n][n][128]
@@ -96,6 +118,9 @@ struct GridAttentionArgs {
   int64_t osb, ost, ohs;     // out element (b, t, h, d) at out[b*osb + t*ost + h*ohs + d], d < Dv
   int64_t mbs;
   int B, H, Nq, N, Npad, Nblk, Dv;
+  // Optional gate in out's layout: out = sigmoid(gate) * attention (the gating Linear of
+  // SelfAttention applied at the store).
+  const bf16 *gate = nullptr;
 };
 // Fused grid-attention projection / output (grid_fused.hip), bf16, c = 128, 4 x 32 heads.
 struct GridProjectArgs {

@@ -249,6 +249,57 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
   return mha_attention(ga, pl.D, s);
 }
 
+// ---- self-attention on operands projected straight into the kernel's layouts
+
+namespace {
+
+// words[b][w]: one wavefront per word, lane j = key 64 w + j.
+__global__ void mask_words_kernel(const void *__restrict__ mask, int dtype, int64_t stride, int64_t rows,
+                                  int64_t T, int64_t nblk, uint64_t *__restrict__ words) {
+  const int64_t word = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) >> 6;
+  if (word >= rows * nblk) return;
+  const int64_t b = word / nblk, key = (word % nblk) * 64 + (threadIdx.x & 63);
+  const bool keep = key < T && (!mask || load_any(mask, dtype, b * stride + key) != 0.f);
+  const uint64_t ballot = __ballot(keep);
+  if ((threadIdx.x & 63) == 0) words[word] = ballot;
+}
+
+}  // namespace
+
+int attention_operands_dims(int64_t T, int64_t Dh, int *dp, int64_t *tpad) {
+  if (Dh <= 0 || Dh % 4 || padded_dim(Dh) == 0) return fail(XFH_EUNSUPPORTED, "attention operands: head dim must be a multiple of 4, at most 64");
+  if (T <= 0 || align_up(T, 64) > grid_attention_max_n())
+    return fail(XFH_EUNSUPPORTED, "attention operands: token count outside (0, xfh_attention_max_keys()]");
+  *dp = padded_dim(Dh);
+  *tpad = align_up(T, 64);
+  return XFH_OK;
+}
+
+int attention_mask_words(const void *mask, int dtype, int64_t stride, int64_t rows, int64_t T, uint64_t *words,
+                         hipStream_t s) {
+  const int64_t nblk = ceil_div(T, 64), blocks = ceil_div(rows * nblk * 64, 256);
+  if (blocks == 0) return XFH_OK;
+  if (blocks > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, "attention_mask_words: problem too large");
+  mask_words_kernel<<<dim3(unsigned(blocks)), 256, 0, s>>>(mask, dtype, stride, rows, T, nblk, words);
+  return check_launch("attention_mask_words");
+}
+
+int attention_operands(const bf16 *q, const bf16 *k, const bf16 *vt, const uint64_t *words, bool words_shared,
+                       const float *bias, const bf16 *gate, bf16 *out, int64_t B, int64_t T, int64_t H, int64_t Dh,
+                       hipStream_t s) {
+  int dp = 0;
+  int64_t tpad = 0;
+  XFH_TRY(attention_operands_dims(T, Dh, &dp, &tpad));
+  GridAttentionArgs ga;
+  ga.q = q; ga.k = k; ga.vt = vt; ga.maskbits = words; ga.bias = bias; ga.gate = gate;
+  ga.out = out;
+  ga.osb = T * H * Dh; ga.ost = H * Dh; ga.ohs = Dh;
+  ga.mbs = words_shared ? 0 : tpad / 64;
+  ga.B = int(B); ga.H = int(H); ga.Nq = int(T); ga.N = int(T);
+  ga.Npad = int(tpad); ga.Nblk = int(tpad / 64); ga.Dv = int(Dh);
+  return mha_attention(ga, dp, s);
+}
+
 namespace {
 
 // Bias packing: thread = (q, key) over keys < npad, reading all G*H heads of a bf16 view whose

@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 F32, BF16, BOOL = 0, 1, 2
 BIAS_PACKED = 3                 # bias 'dtype' of a block written by xfh_attention_bias_pack
@@ -55,6 +55,10 @@ SIGNATURES = {
     "xfh_dot_product_attention": (_i, [_p, _p, _p, _i, _p, _i, _p, _i, _p, _i, _pi64, _pi64, _f, _p, _i64, _p]),
     "xfh_attention_max_keys": (_i64, []),
     "xfh_attention_bias_pack": (_i, [_p, _i, _pi64, _pi64, _p, _p]),
+    "xfh_attention_operands_size": (_i, [_i64, _i64, _i64, _i64, _pi64]),
+    "xfh_attention_project": (_i, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _p, _p, _p, _p, _p]),
+    "xfh_attention_mask_words": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
+    "xfh_attention_operands": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
     "xfh_pair_attention_bias": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _i64, _p, _p]),
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
     "xfh_triangle_multiplication": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,

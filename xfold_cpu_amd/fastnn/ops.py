@@ -194,6 +194,88 @@ def pair_attention_bias(pair: torch.Tensor, ln_w: Optional[torch.Tensor], ln_b: 
     return out
 
 
+class AttentionOperands:
+    """Buffers of one self-attention call in the pipelined attention kernel's own layouts
+    (``xfh_attention_operands_size``), for B samples of T tokens and H heads of Dh: q
+    [B, H, T, Dp], k [B, H, Tpad, Dp], v^T [B, H, Dp, Tpad] (zero-initialised: the projection
+    never writes their padding, so one set serves every call of that shape), the gate
+    [B, T, H*Dh] and the kept-key words of the current mask."""
+
+    def __init__(self, B: int, T: int, H: int, Dh: int, device: torch.device):
+        sizes = (ctypes.c_int64 * 5)()
+        nh.call("xfh_attention_operands_size", B, T, H, Dh, sizes)
+        self.shape = (B, T, H, Dh)
+        self.device = torch.device(device)
+        self.dp, self.tpad = int(sizes[0]), int(sizes[1])
+        self.q = torch.zeros(int(sizes[2]), dtype=torch.bfloat16, device=device)
+        self.k = torch.zeros(int(sizes[3]), dtype=torch.bfloat16, device=device)
+        self.vt = torch.zeros(int(sizes[4]), dtype=torch.bfloat16, device=device)
+        self.gate = torch.empty((B, T, H * Dh), dtype=torch.bfloat16, device=device)
+        self.words = torch.empty(B * (self.tpad // 64), dtype=torch.int64, device=device)
+        self.words_shared = True
+        self._mask_key = ()
+
+    @staticmethod
+    def supported(T: int, H: int, Dh: int) -> bool:
+        return Dh % 4 == 0 and 0 < Dh <= 64 and 0 < T and (T + 63) // 64 * 64 <= nh.attention_max_keys()
+
+    def matches(self, B: int, T: int, H: int, Dh: int, device: torch.device) -> bool:
+        return self.shape == (B, T, H, Dh) and self.device == torch.device(device)
+
+    def set_mask(self, mask: Optional[torch.Tensor]) -> None:
+        """Kept-key words of a key mask: None, [T] (shared by the samples) or [B, T]."""
+        # Inference tensors carry no version counter: their words are recomputed every time.
+        key = (None,) if mask is None else \
+            None if mask.is_inference() else (mask.data_ptr(), mask._version, tuple(mask.shape), mask.dtype)
+        if key is not None and key == self._mask_key:
+            return
+        B, T = self.shape[0], self.shape[1]
+        rows, code, m = 1, nh.BOOL, None
+        if mask is not None:
+            if mask.dim() == 2 and tuple(mask.shape) == (B, T):
+                rows = B
+            elif tuple(mask.shape) != (T,):
+                raise ValueError(f"attention operands: mask must be [{T}] or [{B}, {T}]")
+            if mask.dtype not in (torch.bool, torch.uint8, torch.float32, torch.bfloat16):
+                mask = mask.to(torch.bool)
+            m = mask.contiguous()
+            code = nh.BOOL if m.dtype in (torch.bool, torch.uint8) else nh.dtype_code(m.dtype)
+        nh.call("xfh_attention_mask_words", nh.ptr(m), code, T, rows, T, nh.ptr(self.words),
+                nh.stream_of(self.device))
+        self.words_shared = rows == 1
+        self._mask_key = key
+
+
+def attention_project(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],
+                      operands: AttentionOperands, qscale: float) -> None:
+    """[q | k | v | gate] = x @ weight^T + bias straight into ``operands`` (one GEMM); x
+    [B*T, K] (or [B, T, K]) bf16, weight [4*H*Dh, K] bf16, bias fp32 [4*H*Dh] or None."""
+    B, T, H, Dh = operands.shape
+    k_dim = x.shape[-1]
+    if x.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16 or tuple(weight.shape) != (4 * H * Dh, k_dim):
+        raise ValueError("attention_project: bf16 x and a [4*H*Dh, K] bf16 weight")
+    x_c = x.contiguous()
+    if x_c.numel() != B * T * k_dim:
+        raise ValueError("attention_project: x must hold B*T rows")
+    b = None if bias is None else bias.detach().to(torch.float32).contiguous()
+    nh.call("xfh_attention_project", nh.ptr(x_c), k_dim, nh.ptr(weight.contiguous()), nh.ptr(b), B, T, k_dim, H, Dh,
+            float(qscale), nh.ptr(operands.q), nh.ptr(operands.k), nh.ptr(operands.vt), nh.ptr(operands.gate),
+            nh.stream_of(x.device))
+
+
+def attention_on_operands(operands: AttentionOperands, bias: PackedBias, out: torch.Tensor) -> torch.Tensor:
+    """out [B, T, H*Dh] bf16 = sigmoid(gate) * attention over ``operands`` with a packed bias."""
+    B, T, H, Dh = operands.shape
+    if not isinstance(bias, PackedBias) or tuple(bias.tensor.shape) != (H, T, operands.tpad):
+        raise ValueError("attention_on_operands: bias must be a packed [H, T, align64(T)] block")
+    if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != B * T * H * Dh:
+        raise ValueError("attention_on_operands: out must be a contiguous bf16 [B, T, H*Dh]")
+    nh.call("xfh_attention_operands", nh.ptr(operands.q), nh.ptr(operands.k), nh.ptr(operands.vt),
+            nh.ptr(operands.words), int(operands.words_shared), nh.ptr(bias.tensor), nh.ptr(operands.gate),
+            nh.ptr(out), B, T, H, Dh, nh.stream_of(out.device))
+    return out
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[torch.Tensor],
               bias: Optional[torch.Tensor], out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:

@@ -127,11 +127,11 @@ class InputCache:
         if not config.input_cache_enabled or scope is None or owner.training or torch.is_grad_enabled():
             self.clear()
             return factory()
-        members = []
+        members = {}                          # id -> module, in first-seen order
         for module in ((owner,) if modules is None else modules):
             for child in module.modules():
-                if child not in members:
-                    members.append(child)
+                members.setdefault(id(child), child)
+        members = list(members.values())
         if any(m.training for m in members):
             self.clear()
             return factory()

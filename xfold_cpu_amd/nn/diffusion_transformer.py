@@ -94,14 +94,40 @@ def diffusion_transition_hip(module: nn.Module, x: torch.Tensor, single_cond=Non
 _QKV = ("q_projection", "k_projection", "v_projection")
 
 
+def _projection_bias(module: nn.Module, c: int, parts: int, device: torch.device) -> Optional[torch.Tensor]:
+    """fp32 bias of the stacked [q | k | v (| gate)] projection: q_projection's bias, zeros
+    for the rest (k, v and the gate have none), cached while the bias is unchanged."""
+    q_bias = module.q_projection.bias
+    if q_bias is None:
+        return None
+    cached = module.__dict__.get(f"_hip_proj_bias{parts}")
+    key = (q_bias.data_ptr(), q_bias._version) if not q_bias.is_inference() else None
+    if cached is None or key is None or cached[0] != key:
+        full = torch.zeros(parts * c, dtype=torch.float32, device=device)
+        full[:c] = q_bias.detach().to(torch.float32)
+        cached = (key, full)
+        if key is not None:
+            module.__dict__[f"_hip_proj_bias{parts}"] = cached
+    return cached[1]
+
+
+_LOG2E = 1.4426950408889634
+
+
 def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.Tensor],
                        pair_logits: Optional[torch.Tensor] = None,
                        single_cond: Optional[torch.Tensor] = None,
                        accumulate_into: Optional[torch.Tensor] = None, *,
-                       _cond: Optional[tuple] = None) -> torch.Tensor:
+                       _cond: Optional[tuple] = None,
+                       _operands: Optional[ops.AttentionOperands] = None) -> torch.Tensor:
     """``SelfAttention.forward`` (``diffusion_transformer.py:184-217``) for x [N, c] or
     [S, N, c]; pair_logits [H, N, N] is the attention bias, mask [N] the key mask.
-    ``_cond`` = (scale, shift, zero_cond) precomputed by :func:`_block_conditioning`."""
+    ``_cond`` = (scale, shift, zero_cond) precomputed by :func:`_block_conditioning`.
+
+    With bf16, a packed bias and head dims the pipelined kernel takes, the q/k/v and gating
+    projections are one GEMM writing the attention kernel's layouts, and the gate is applied
+    at the attention's store. ``_operands`` (an :class:`ops.AttentionOperands` of this shape,
+    its mask words already set) lets a caller reuse one set of buffers over many blocks."""
     logits_t = pair_logits.tensor if isinstance(pair_logits, ops.PackedBias) else pair_logits
     nh.check_gpu_inference(x, mask, logits_t, single_cond, *module.parameters())
     dtype = nh.compute_dtype(x, *(getattr(module, n).weight for n in _QKV + ("gating_query",)))
@@ -114,19 +140,20 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
     d = c // heads
     xn = _adaptive_layer_norm(module.adaptive_layernorm, x, single_cond, dtype,
                               cond=None if _cond is None else _cond[:2])
+    if dtype == torch.bfloat16 and isinstance(pair_logits, ops.PackedBias) and c % 32 == 0 and \
+            ops.AttentionOperands.supported(n, heads, d) and \
+            (mask is None or tuple(mask.shape) in ((n,), (samples, n))):
+        operands = _operands
+        if operands is None or not operands.matches(samples, n, heads, d, x.device):
+            operands = ops.AttentionOperands(samples, n, heads, d, x.device)
+        operands.set_mask(mask)
+        w_all = nh.fused_linear_weight(module, _QKV + ("gating_query",), dtype)
+        ops.attention_project(xn, w_all, _projection_bias(module, c, 4, x.device), operands, d ** -0.5 * _LOG2E)
+        o = ops.attention_on_operands(operands, pair_logits, torch.empty((samples, n, c), dtype=dtype, device=x.device))
+        return _ada_ln_zero(module.adaptive_zero_init, o.reshape(x.shape), single_cond, dtype, accumulate_into,
+                            cond=None if _cond is None else _cond[2])
     w_qkv = nh.fused_linear_weight(module, _QKV, dtype)
-    q_bias = module.q_projection.bias
-    bias_qkv = None
-    if q_bias is not None:
-        bias_qkv = module.__dict__.get("_hip_qkv_bias")
-        key = (q_bias.data_ptr(), q_bias._version) if not q_bias.is_inference() else None
-        if bias_qkv is None or key is None or bias_qkv[0] != key:
-            full = torch.zeros(3 * c, dtype=torch.float32, device=x.device)
-            full[:c] = q_bias.detach().to(torch.float32)
-            bias_qkv = (key, full)
-            if key is not None:
-                module.__dict__["_hip_qkv_bias"] = bias_qkv
-        bias_qkv = bias_qkv[1]
+    bias_qkv = _projection_bias(module, c, 3, x.device)
     qkv = ops.linear(xn, w_qkv, bias_qkv, dtype)                     # [.., N, 3c]
     qkv = qkv.reshape(samples, n, 3 * c)
     row = 3 * c
@@ -225,6 +252,20 @@ def _cached(module: nn.Module, name: str, dependencies, factory, modules):
     return cache.get(name, dependencies, module, factory, modules=modules)
 
 
+def _block_operands(module: nn.Module, act: torch.Tensor, mask: Optional[torch.Tensor]):
+    """One set of attention-operand buffers (and mask words) for every block of a forward,
+    or None when the blocks' attention takes the general path."""
+    samples = 1 if act.dim() == 2 else act.shape[0]
+    n, c, heads = act.shape[-2], act.shape[-1], module.num_head
+    if c % heads or not ops.AttentionOperands.supported(n, heads, c // heads):
+        return None
+    if mask is not None and tuple(mask.shape) not in ((n,), (samples, n)):
+        return None
+    operands = ops.AttentionOperands(samples, n, heads, c // heads, act.device)
+    operands.set_mask(mask)
+    return operands
+
+
 def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.Tensor,
                               single_cond: torch.Tensor, pair_cond: torch.Tensor) -> torch.Tensor:
     """``DiffusionTransformer.forward`` (``diffusion_transformer.py:250-272``), updating
@@ -259,16 +300,18 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         packed = _cached(module, "pair_logits_packed", (pair_cond, heads),
                          lambda: ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln),
                          modules=(ln, module.pair_logits_projection))
+        operands = _block_operands(module, act, mask)
         for index in range(n_blocks):
             att_cond, tr_cond = (None, None) if conds is None else conds[index]
             bias = ops.PackedBias(packed[index * heads:(index + 1) * heads])
             self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
-                               accumulate_into=act, _cond=att_cond)
+                               accumulate_into=act, _cond=att_cond, _operands=operands)
             diffusion_transition_hip(module.transition_block[index], act, single_cond,
                                      accumulate_into=act, _cond=tr_cond)
         return act
     pair_act = ops.layer_norm(pair_cond, ln.normalized_shape, ln.weight, ln.bias, ln.eps,
                               out_dtype=dtype, owner=ln)
+    operands = _block_operands(module, act, mask) if packed_bias else None
     for s in range(module.num_super_blocks):
         weight = nh.linear_weight(module.pair_logits_projection, str(s), dtype)
         logits = ops.linear(pair_act, weight, None, dtype)               # [N, N, size*heads]
@@ -285,7 +328,7 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
             index = s * size + j
             att_cond, tr_cond = (None, None) if conds is None else conds[index]
             self_attention_hip(module.self_attention[index], act, mask, bias, single_cond,
-                               accumulate_into=act, _cond=att_cond)
+                               accumulate_into=act, _cond=att_cond, _operands=operands)
             diffusion_transition_hip(module.transition_block[index], act, single_cond,
                                      accumulate_into=act, _cond=tr_cond)
     return act
