@@ -31,8 +31,11 @@ extern "C" {
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
 
-/* Bias "dtype" of xfh_dot_product_attention for a bias written by xfh_attention_bias_pack. */
+/* Bias "dtype" of xfh_dot_product_attention for a packed bias block [H][Q][align64(K)]:
+ * fp32 times log2(e) (xfh_attention_bias_pack, xfh_pair_attention_bias with out_dtype
+ * XFH_F32), or bf16 in natural units (xfh_pair_attention_bias with out_dtype XFH_BF16). */
 #define XFH_BIAS_PACKED 3
+#define XFH_BIAS_PACKED_BF16 4
 
 /* GEMM epilogues of xfh_linear: acc = x @ w^T + bias, a = aux[row % aux_rows, col]. */
 enum {
@@ -122,9 +125,9 @@ int xfh_gated_linear_unit(const void *x, const void *w_packed, int64_t m, int64_
  * mask that depends on the batch entry and key only (the single-track and diffusion
  * shapes), a workspace of xfh_dot_product_attention_workspace_size(shape, dtype) bytes
  * selects the pipelined kernel; other calls, or workspace = NULL, use the general one.
- * bias_dtype = XFH_BIAS_PACKED: bias points at one [H][Q][align64(K)] block written by
- * xfh_attention_bias_pack (bias strides ignored); such calls must take the pipelined kernel
- * and fail with XFH_EUNSUPPORTED otherwise. */
+ * bias_dtype = XFH_BIAS_PACKED or XFH_BIAS_PACKED_BF16: bias points at one [H][Q][align64(K)]
+ * packed block (bias strides ignored); such calls must take the pipelined kernel and fail
+ * with XFH_EUNSUPPORTED otherwise. */
 int64_t xfh_dot_product_attention_workspace_size(const int64_t *shape, int dtype);
 int xfh_dot_product_attention(const void *q, const void *k, const void *v, int dtype,
                               const void *mask, int mask_dtype, const void *bias, int bias_dtype,
@@ -180,25 +183,27 @@ int xfh_attention_mask_words(const void *mask, int mask_dtype, int64_t mask_stri
 /* out [B][T][H*Dh] bf16 = softmax(q k^T + bias, masked keys removed) v over operands written
  * by xfh_attention_project (q already scaled), times sigmoid(gate) elementwise when gate is
  * given (gate [B][T][H*Dh] bf16: SelfAttention's gating, diffusion_transformer.py:209-211).
- * bias = one packed [H][T][Tpad] block (xfh_attention_bias_pack, xfh_pair_attention_bias),
- * required; words from xfh_attention_mask_words with rows = B, or rows = 1 and
+ * bias = one packed [H][T][Tpad] block of bias_dtype XFH_BIAS_PACKED or XFH_BIAS_PACKED_BF16
+ * (xfh_attention_bias_pack, xfh_pair_attention_bias), required; words from xfh_attention_mask_words with rows = B, or rows = 1 and
  * words_shared = 1 for a mask shared by the samples. A row whose keys are all masked
  * averages v uniformly, as the reference's -1e9 fill does. */
 int xfh_attention_operands(const void *q, const void *k, const void *vt, const uint64_t *words, int words_shared,
-                           const float *bias, const void *gate, void *out, int64_t B, int64_t T, int64_t H,
-                           int64_t Dh, void *stream);
+                           const void *bias, int bias_dtype, const void *gate, void *out, int64_t B, int64_t T,
+                           int64_t H, int64_t Dh, void *stream);
 
-/* Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' straight into the packed bias layout
- * of xfh_attention_bias_pack: packed[h][i][j] fp32 = log2(e) * (LN(pair[i][j]) . w[h]) for
- * j < n, 0 for n <= j < align64(n); pair contiguous [n, n, c] (f32/bf16, c = 128), LayerNorm
- * affine ln_w/ln_b (fp32, may be null), w bf16 [heads][c] (heads <= 384), computed in bf16
- * with fp32 accumulation. Each block of heads is then an XFH_BIAS_PACKED bias. Replaces the
- * pair-logits path of PairformerBlock's single-track attention
+/* Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' straight into a packed bias layout:
+ * with out_dtype XFH_F32, packed[h][i][j] fp32 = log2(e) * (LN(pair[i][j]) . w[h]) (the
+ * layout of xfh_attention_bias_pack, an XFH_BIAS_PACKED bias per block of heads); with
+ * XFH_BF16, packed[h][i][j] bf16 = LN(pair[i][j]) . w[h] (an XFH_BIAS_PACKED_BF16 bias,
+ * rounded where the reference's autocast Linear rounds its output); 0 for n <= j <
+ * align64(n). pair contiguous [n, n, c] (f32/bf16, c = 128), LayerNorm affine ln_w/ln_b
+ * (fp32, may be null), w bf16 [heads][c] (heads <= 384), computed in bf16 with fp32
+ * accumulation. Replaces the pair-logits path of PairformerBlock's single-track attention
  * (xfold/nn/pairformer.py:103-106) and of DiffusionTransformer
  * (xfold/nn/diffusion_transformer.py:258-271, all super-blocks' projections stacked). */
 int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t c, const float *ln_w,
                             const float *ln_b, float eps, const void *w, int w_dtype, int64_t heads,
-                            void *packed, void *stream);
+                            void *packed, int out_dtype, void *stream);
 
 /* Triangle multiplication update of a contiguous [n, n, c] pair tensor (mask [n, n]).
  * out (contiguous [n, n, c]) receives the update, or the update is added to it when

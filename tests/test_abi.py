@@ -114,6 +114,15 @@ def test_guards_reject_cpu_tensors_and_gradients():
         fastnn.dot_product_attention(torch.randn(1, 1, 2, 4), torch.randn(1, 1, 2, 4), torch.randn(1, 1, 2, 4))
     with torch.enable_grad(), pytest.raises(RuntimeError, match="inference only"):
         nh.check_gpu_inference(torch.randn(2, requires_grad=True, device="meta"))
+    # A module's parameters are checked in grad mode only; a host tensor never gets a pointer.
+    lin = torch.nn.Linear(2, 2)
+    with torch.enable_grad(), pytest.raises(RuntimeError, match="inference only"):
+        nh.check_module(lin)
+    with torch.no_grad():
+        nh.check_module(lin)
+    with pytest.raises(ValueError, match="ROCm"):
+        nh.ptr(lin.weight)
+    assert nh.ptr(None) is None
 
 
 def test_compute_dtype_rules():

@@ -224,9 +224,8 @@ def test_unpacked_bias_beyond_the_attention_key_limit(device, monkeypatch):
 
 def test_diffusion_input_cache_skips_the_pair_logits_on_repeat_calls(device):
     """Inside an input-cache scope (the reference's InputCache rules) a second call with the
-    same pair_cond, single_cond and weights reuses the packed pair logits and the block
-    conditioning (no pair_bias_kernel launch) and gives the same result bit for bit; an
-    in-place update of pair_cond invalidates them."""
+    same pair_cond and weights reuses the packed pair logits (no pair_bias_kernel launch)
+    and gives the same result bit for bit; an in-place update of pair_cond invalidates them."""
     from xfold_cpu_amd.fastnn import config
     from xfold_cpu_amd.fastnn import native_hip as nh
     from xfold_cpu_amd.nn.cache import input_cache_scope

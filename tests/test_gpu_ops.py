@@ -195,23 +195,48 @@ def test_gated_linear_unit(device, m, k, f, dtype):
 
 @pytest.mark.parametrize("n,heads", [(70, 16), (33, 20), (128, 384)])
 @pytest.mark.parametrize("pair_dtype", [torch.float32, torch.bfloat16])
-def test_pair_attention_bias(device, n, heads, pair_dtype):
-    """Linear(LayerNorm(pair)) rearranged to [h, i, j], times log2(e), in the packed layout
-    with zero pad columns (xfold/nn/pairformer.py:103-106)."""
-    announce("pair_attention_bias", n, heads, pair_dtype)
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_pair_attention_bias(device, n, heads, pair_dtype, out_dtype):
+    """Linear(LayerNorm(pair)) rearranged to [h, i, j] in the packed layout with zero pad
+    columns (xfold/nn/pairformer.py:103-106): fp32 times log2(e), or bf16 logits."""
+    announce("pair_attention_bias", n, heads, pair_dtype, out_dtype)
     g = torch.Generator().manual_seed(n + heads)
     pair = (torch.randn(n, n, 128, generator=g) * 2 + 0.5).to(pair_dtype)
     ln_w, ln_b = 1 + 0.1 * torch.randn(128, generator=g), 0.1 * torch.randn(128, generator=g)
     w = (torch.randn(heads, 128, generator=g) / math.sqrt(128)).bfloat16()
+    scale = math.log2(math.e) if out_dtype == torch.float32 else 1.0
     def oracle():
         out = F.layer_norm(pair.float(), (128,), ln_w, ln_b, 1e-5) @ w.float().T
-        return out.permute(2, 0, 1) * math.log2(math.e)
+        return out.permute(2, 0, 1) * scale
     want, floor = oracle(), floor_of(oracle)
-    got = ops.pair_attention_bias(pair.to(device), ln_w.to(device), ln_b.to(device), 1e-5, w.to(device))
+    got = ops.pair_attention_bias(pair.to(device), ln_w.to(device), ln_b.to(device), 1e-5, w.to(device),
+                                  out_dtype=out_dtype)
     npad = (n + 63) // 64 * 64
-    assert got.shape == (heads, n, npad)
+    assert got.shape == (heads, n, npad) and got.dtype == out_dtype
     assert bool((got[..., n:] == 0).all())
+    if out_dtype == torch.bfloat16:
+        floor = bf16_stored(floor)
     assert_parity_bf16(got[..., :n], want, "pair_attention_bias", floor=floor)
+
+
+@pytest.mark.parametrize("d", [32, 48, 64])
+@pytest.mark.parametrize("batch", [1, 3])
+def test_attention_packed_bias_bf16(device, d, batch):
+    """A bf16 packed bias (natural units, widened and scaled by log2(e) in the kernel) gives
+    the same bits as the fp32 packed bias of the same bf16 logits."""
+    announce("attention packed bias bf16", d, batch)
+    g = torch.Generator().manual_seed(d + batch)
+    H, N = 4, 100
+    npad = 128
+    q, k, v = (torch.randn(batch, H, N, d, generator=g).bfloat16().to(device) for _ in range(3))
+    mask = (torch.rand(batch, N, generator=g) > 0.2).to(device)
+    logits = (torch.randn(H, N, N, generator=g) * 3).bfloat16().to(device)
+    packed32 = ops.PackedBias(ops.attention_bias_pack(logits[None])[0])
+    packed16 = ops.PackedBias(F.pad(logits, (0, npad - N)).contiguous())
+    assert packed16.code == nh.BIAS_PACKED_BF16
+    want = ops.attention(q, k, v, mask, packed32)
+    got = ops.attention(q, k, v, mask, packed16)
+    assert torch.equal(got, want), f"max diff {(got.float() - want.float()).abs().max().item()}"
 
 
 @pytest.mark.parametrize("d", [32, 48, 64])

@@ -302,7 +302,8 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   XFH_REQUIRE(shape && strides, "dot_product_attention: null shape/strides");
   XFH_REQUIRE(float_dtype(dtype), "dot_product_attention: dtype must be f32/bf16");
   XFH_REQUIRE(!mask || mask_dtype_ok(mask_dtype), "dot_product_attention: bad mask dtype");
-  XFH_REQUIRE(!bias || float_dtype(bias_dtype) || bias_dtype == XFH_BIAS_PACKED,
+  XFH_REQUIRE(!bias || float_dtype(bias_dtype) || bias_dtype == XFH_BIAS_PACKED ||
+                  bias_dtype == XFH_BIAS_PACKED_BF16,
               "dot_product_attention: bias must be f32/bf16 or packed");
   AttentionArgs a;
   std::memset(&a, 0, sizeof(a));
@@ -324,7 +325,7 @@ int xfh_dot_product_attention(const void *q, const void *k, const void *v, int d
   // workspace of xfh_dot_product_attention_workspace_size bytes; the rest, or a call
   // without workspace, on the general kernel.
   if (workspace && mha_supported(a, dtype)) return mha(a, workspace, workspace_bytes, as_stream(stream));
-  if (bias && bias_dtype == XFH_BIAS_PACKED)
+  if (bias && (bias_dtype == XFH_BIAS_PACKED || bias_dtype == XFH_BIAS_PACKED_BF16))
     return fail(XFH_EUNSUPPORTED, "dot_product_attention: a packed bias needs the pipelined kernel "
                                   "(bf16, head dim <= 64, workspace given)");
   return attention(a, dtype, as_stream(stream));
@@ -393,23 +394,26 @@ int xfh_attention_mask_words(const void *mask, int mask_dtype, int64_t mask_stri
 }
 
 int xfh_attention_operands(const void *q, const void *k, const void *vt, const uint64_t *words, int words_shared,
-                           const float *bias, const void *gate, void *out, int64_t B, int64_t T, int64_t H,
-                           int64_t Dh, void *stream) {
+                           const void *bias, int bias_dtype, const void *gate, void *out, int64_t B, int64_t T,
+                           int64_t H, int64_t Dh, void *stream) {
   XFH_REQUIRE(B >= 0 && H > 0, "attention_operands: bad sizes");
+  XFH_REQUIRE(bias_dtype == XFH_BIAS_PACKED || bias_dtype == XFH_BIAS_PACKED_BF16,
+              "attention_operands: the bias must be packed (XFH_BIAS_PACKED or XFH_BIAS_PACKED_BF16)");
   if (B == 0) return XFH_OK;
   XFH_REQUIRE(q && k && vt && words && bias && out, "attention_operands: null tensor (the bias is required)");
   XFH_REQUIRE(reinterpret_cast<uintptr_t>(out) % 8 == 0 && (!gate || reinterpret_cast<uintptr_t>(gate) % 8 == 0),
               "attention_operands: out and gate must be 8-byte aligned");
   return attention_operands(static_cast<const bf16 *>(q), static_cast<const bf16 *>(k),
                             static_cast<const bf16 *>(vt), words, words_shared != 0, bias,
-                            static_cast<const bf16 *>(gate), static_cast<bf16 *>(out), B, T, H, Dh,
-                            as_stream(stream));
+                            bias_dtype == XFH_BIAS_PACKED_BF16, static_cast<const bf16 *>(gate),
+                            static_cast<bf16 *>(out), B, T, H, Dh, as_stream(stream));
 }
 
 int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t c, const float *ln_w,
                             const float *ln_b, float eps, const void *w, int w_dtype, int64_t heads,
-                            void *packed, void *stream) {
+                            void *packed, int out_dtype, void *stream) {
   XFH_REQUIRE(float_dtype(pair_dtype), "pair_attention_bias: pair dtype must be f32/bf16");
+  XFH_REQUIRE(float_dtype(out_dtype), "pair_attention_bias: out dtype must be f32/bf16");
   XFH_REQUIRE(w_dtype == XFH_BF16, "pair_attention_bias: the weight must be bf16");
   XFH_REQUIRE(c == 128, "pair_attention_bias: 128 pair channels");
   XFH_REQUIRE(heads > 0 && heads <= pair_bias_max_heads(), "pair_attention_bias: 1..384 heads");
@@ -419,7 +423,7 @@ int xfh_pair_attention_bias(const void *pair, int pair_dtype, int64_t n, int64_t
   XFH_REQUIRE(pair && w && packed, "pair_attention_bias: null tensor");
   PairBiasArgs a;
   a.pair = pair; a.ln_w = ln_w; a.ln_b = ln_b; a.eps = eps;
-  a.w = static_cast<const bf16 *>(w); a.packed = static_cast<float *>(packed);
+  a.w = static_cast<const bf16 *>(w); a.packed = packed; a.packed_bf16 = out_dtype == XFH_BF16;
   a.n = int(n); a.npad = int(align_up(n, 64)); a.heads = int(heads);
   return pair_bias(a, pair_dtype, as_stream(stream));
 }

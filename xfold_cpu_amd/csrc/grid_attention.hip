@@ -119,7 +119,19 @@ __device__ __forceinline__ float max16(const f32x4 (&s)[4]) {
   return vmax(m, s[3][3]);
 }
 
-template <class S>
+template <typename BT> __device__ __forceinline__ f32x4 bias_quad(const BT *p);
+template <> __device__ __forceinline__ f32x4 bias_quad<float>(const float *p) {
+  return *reinterpret_cast<const f32x4 *>(p);
+}
+// bf16 bias in natural units: widened and taken to log2 units here.
+template <> __device__ __forceinline__ f32x4 bias_quad<bf16>(const bf16 *p) {
+  const bf16x4 v = *reinterpret_cast<const bf16x4 *>(p);
+  constexpr float kLog2e = 1.4426950408889634f;
+  return f32x4{static_cast<float>(v[0]) * kLog2e, static_cast<float>(v[1]) * kLog2e,
+               static_cast<float>(v[2]) * kLog2e, static_cast<float>(v[3]) * kLog2e};
+}
+
+template <class S, typename BT = float>
 __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAttentionArgs a) {
   constexpr int R = S::R, W = S::W, TQ = S::TQ, GQ = S::Q, STAGE = S::STAGE, D = S::D;
   constexpr int K_ELEMS = S::K_ELEMS, V_ELEMS = S::V_ELEMS, DT = S::DT, KS = S::KS;
@@ -265,11 +277,11 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
   auto drain = [] { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); };
   // Bias tile of query tile tq: [16 queries x 64 keys], lane (col, grp) holds keys
   // kt*16 + grp*4 + 0..3 of query q0 + 16 tq + col.
-  const float *bias_rows[TQ];
+  const BT *bias_rows[TQ];
 #pragma unroll
   for (int tq = 0; tq < TQ; ++tq) {
     const int q = q0 + 16 * tq + col;
-    bias_rows[tq] = a.bias + (int64_t(h) * a.Nq + (q < a.Nq ? q : a.Nq - 1)) * a.Npad;
+    bias_rows[tq] = static_cast<const BT *>(a.bias) + (int64_t(h) * a.Nq + (q < a.Nq ? q : a.Nq - 1)) * a.Npad;
   }
   f32x4 bias[TQ][4];
   auto load_bias = [&](int kb) {
@@ -277,7 +289,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
     for (int tq = 0; tq < TQ; ++tq)
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt)
-        bias[tq][kt] = *reinterpret_cast<const f32x4 *>(bias_rows[tq] + kb * GKB + kt * 16 + grp * 4);
+        bias[tq][kt] = bias_quad<BT>(bias_rows[tq] + kb * GKB + kt * 16 + grp * 4);
   };
 
   // S^T of row r (+ the additive mask row when masked), both query tiles.
@@ -489,7 +501,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
 
 int64_t grid_attention_pad_(int64_t n) { return align_up(n, GKB); }
 
-template <class S> int launch(const GridAttentionArgs &a, const char *name, hipStream_t s) {
+template <class S, typename BT = float> int launch(const GridAttentionArgs &a, const char *name, hipStream_t s) {
   if (a.B == 0 || a.Nq == 0 || a.N == 0) return XFH_OK;
   if (a.Nblk > kMaxKeyBlocks) return fail(XFH_EUNSUPPORTED, std::string(name) + ": more than 4096 keys");
   const int64_t qblocks = ceil_div(a.Nq, S::Q), rgroups = ceil_div(a.B, S::R);
@@ -497,13 +509,14 @@ template <class S> int launch(const GridAttentionArgs &a, const char *name, hipS
   const int64_t grid = ceil_div(total, 8) * 8;
   if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, std::string(name) + ": problem too large");
   KernelTimer timer(name, s);
-  grid_attention_kernel<S><<<dim3(grid), S::T, 0, s>>>(a);
+  grid_attention_kernel<S, BT><<<dim3(grid), S::T, 0, s>>>(a);
   return check_launch(name);
 }
 
 }  // namespace
 
 int grid_attention(const GridAttentionArgs &a, hipStream_t s) {
+  if (a.bias_bf16) return fail(XFH_EUNSUPPORTED, "grid_attention: fp32 bias only");
   return launch<GridShape>(a, "grid_attention", s);
 }
 
@@ -513,10 +526,15 @@ int mha_attention(const GridAttentionArgs &a, int d, hipStream_t s) {
   // transformer's 5 x 16 heads). At head dim 64, 8 wavefronts (128 queries) share each K/V
   // block: 11% faster per call there than 4.
   if (d == 32) {
-    if (a.B == 1) return launch<Shape<1, 4, 1, 32>>(a, "mha_attention", s);
-    return launch<Shape<4, 4, 1, 32>>(a, "mha_attention", s);
+    if (a.B == 1)
+      return a.bias_bf16 ? launch<Shape<1, 4, 1, 32>, bf16>(a, "mha_attention", s)
+                         : launch<Shape<1, 4, 1, 32>>(a, "mha_attention", s);
+    return a.bias_bf16 ? launch<Shape<4, 4, 1, 32>, bf16>(a, "mha_attention", s)
+                       : launch<Shape<4, 4, 1, 32>>(a, "mha_attention", s);
   }
-  if (d == 64) return launch<Shape<1, 8, 1, 64>>(a, "mha_attention", s);
+  if (d == 64)
+    return a.bias_bf16 ? launch<Shape<1, 8, 1, 64>, bf16>(a, "mha_attention", s)
+                       : launch<Shape<1, 8, 1, 64>>(a, "mha_attention", s);
   return fail(XFH_EUNSUPPORTED, "mha_attention: head dim must be 32 or 64");
 }
 

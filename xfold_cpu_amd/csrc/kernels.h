@@ -92,15 +92,16 @@ int attention_operands_dims(int64_t T, int64_t Dh, int *dp, int64_t *tpad);
 int attention_mask_words(const void *mask, int dtype, int64_t stride, int64_t rows, int64_t T, uint64_t *words,
                          hipStream_t s);
 int attention_operands(const bf16 *q, const bf16 *k, const bf16 *vt, const uint64_t *words, bool words_shared,
-                       const float *bias, const bf16 *gate, bf16 *out, int64_t B, int64_t T, int64_t H, int64_t Dh,
-                       hipStream_t s);
+                       const void *bias, bool bias_bf16, const bf16 *gate, bf16 *out, int64_t B, int64_t T,
+                       int64_t H, int64_t Dh, hipStream_t s);
 // Linear(LayerNorm(pair)) straight into the packed attention-bias layout (pair_bias.hip).
 struct PairBiasArgs {
   const void *pair;          // [n][n][128]
   const float *ln_w, *ln_b;
   float eps;
   const bf16 *w;             // [heads][128]
-  float *packed;             // [heads][n][npad]
+  void *packed;              // [heads][n][npad]: fp32 times log2(e), or bf16 (natural units)
+  int packed_bf16 = 0;
   int n, npad, heads;
 };
 int pair_bias_max_heads();
@@ -112,7 +113,8 @@ int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s);
 // runs of 32, see grid_project); bias [H][Nq][Npad] fp32 times log2(e), shared by all b.
 struct GridAttentionArgs {
   const bf16 *q, *k, *vt;
-  const float *bias;
+  // [H][Nq][Npad]: fp32 times log2(e), or with bias_bf16 bf16 in natural units.
+  const void *bias;
   const uint64_t *maskbits;  // word w of row b at maskbits[b*mbs + w] (mbs 0: one shared row)
   bf16 *out;
   int64_t osb, ost, ohs;     // out element (b, t, h, d) at out[b*osb + t*ost + h*ohs + d], d < Dv
@@ -121,6 +123,7 @@ struct GridAttentionArgs {
   // Optional gate in out's layout: out = sigmoid(gate) * attention (the gating Linear of
   // SelfAttention applied at the store).
   const bf16 *gate = nullptr;
+  int bias_bf16 = 0;
 };
 // Fused grid-attention projection / output (grid_fused.hip), bf16, c = 128, 4 x 32 heads.
 struct GridProjectArgs {

@@ -186,7 +186,8 @@ int64_t mha_workspace_size(const AttentionArgs &a) {
 bool mha_supported(const AttentionArgs &a, int dtype) {
   return dtype == XFH_BF16 && a.out_dtype == XFH_BF16 && padded_dim(a.D > a.Dv ? a.D : a.Dv) != 0 &&
          a.K > 0 && align_up(a.K, 64) <= grid_attention_max_n() &&
-         (!a.bias || a.bias_dtype == XFH_BIAS_PACKED || a.B == 1 || a.bs[0] == 0) &&  // batch-shared bias
+         (!a.bias || a.bias_dtype == XFH_BIAS_PACKED || a.bias_dtype == XFH_BIAS_PACKED_BF16 || a.B == 1 ||
+          a.bs[0] == 0) &&  // batch-shared bias
          // mask per (batch entry, key); a size-1 head or query dimension has no stride to speak of
          (!a.mask || ((a.ms[1] == 0 || a.H == 1) && (a.ms[2] == 0 || a.Q == 1))) &&
          a.os[1] % 4 == 0 && a.os[2] % 4 == 0 && a.os[0] % 4 == 0 &&
@@ -222,7 +223,7 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
   const bool head_minor = a.bias && a.bias_dtype == XFH_BF16 && a.bs[1] == 1 && a.H % 8 == 0 &&
                           a.bs[2] % 8 == 0 && a.bs[3] % 8 == 0 &&
                           reinterpret_cast<uintptr_t>(a.bias) % 16 == 0;
-  const bool packed = a.bias && a.bias_dtype == XFH_BIAS_PACKED;
+  const bool packed = a.bias && (a.bias_dtype == XFH_BIAS_PACKED || a.bias_dtype == XFH_BIAS_PACKED_BF16);
   p.nparts = 0;
   p.start[0] = 0;
   for (int part = 0; part < 5; ++part) {
@@ -240,7 +241,8 @@ int mha(const AttentionArgs &a, void *workspace, int64_t workspace_bytes, hipStr
 
   GridAttentionArgs ga;
   ga.q = p.q; ga.k = p.k; ga.vt = p.vt; ga.maskbits = p.words;
-  ga.bias = packed ? static_cast<const float *>(a.bias) : p.bias;
+  ga.bias = packed ? a.bias : p.bias;
+  ga.bias_bf16 = packed && a.bias_dtype == XFH_BIAS_PACKED_BF16;
   ga.out = static_cast<bf16 *>(a.o);
   ga.osb = a.os[0]; ga.ost = a.os[2]; ga.ohs = a.os[1];
   ga.mbs = per_row ? pl.nblk : 0;
@@ -285,13 +287,13 @@ int attention_mask_words(const void *mask, int dtype, int64_t stride, int64_t ro
 }
 
 int attention_operands(const bf16 *q, const bf16 *k, const bf16 *vt, const uint64_t *words, bool words_shared,
-                       const float *bias, const bf16 *gate, bf16 *out, int64_t B, int64_t T, int64_t H, int64_t Dh,
-                       hipStream_t s) {
+                       const void *bias, bool bias_bf16, const bf16 *gate, bf16 *out, int64_t B, int64_t T,
+                       int64_t H, int64_t Dh, hipStream_t s) {
   int dp = 0;
   int64_t tpad = 0;
   XFH_TRY(attention_operands_dims(T, Dh, &dp, &tpad));
   GridAttentionArgs ga;
-  ga.q = q; ga.k = k; ga.vt = vt; ga.maskbits = words; ga.bias = bias; ga.gate = gate;
+  ga.q = q; ga.k = k; ga.vt = vt; ga.maskbits = words; ga.bias = bias; ga.bias_bf16 = bias_bf16; ga.gate = gate;
   ga.out = out;
   ga.osb = T * H * Dh; ga.ost = H * Dh; ga.ohs = Dh;
   ga.mbs = words_shared ? 0 : tpad / 64;

@@ -283,7 +283,7 @@ int xfh_msa_attention(const void *msa, int msa_dtype, const void *mask, int mask
   if (packed) {
     PairBiasArgs pb;
     pb.pair = pair; pb.ln_w = pair_ln_w; pb.ln_b = pair_ln_b; pb.eps = pair_ln_eps;
-    pb.w = static_cast<const bf16 *>(logits_w); pb.packed = static_cast<float *>(p.logits);
+    pb.w = static_cast<const bf16 *>(logits_w); pb.packed = p.logits; pb.packed_bf16 = 0;
     pb.n = int(n); pb.npad = int(npad); pb.heads = int(heads);
     XFH_TRY(pair_bias(pb, pair_dtype, s));
     logit_dtype = XFH_F32; sh = n * npad; sq = npad; sk = 1;

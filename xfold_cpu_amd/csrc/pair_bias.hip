@@ -1,5 +1,7 @@
 // Pair-logits attention biases straight from the pair tensor (bf16 compute, c = 128):
 //   packed[h][i][j] = log2(e) * sum_k LN(z[i][j])[k] * W[h][k]   (j < n; 0 for n <= j < npad)
+// in fp32, or the sum itself rounded to bf16 (the dtype of the reference's autocast Linear
+// output; the attention kernel applies log2(e) after widening it),
 // i.e. Linear(LayerNorm(pair)) rearranged 'i j h -> h i j' into the attention kernel's bias
 // layout (grid_attention.hip: [H][Nq][Npad] fp32 times log2(e)), for
 //   - PairformerBlock's single-track attention bias (xfold/nn/pairformer.py:103-106), and
@@ -12,6 +14,7 @@
 // after the weight is in. Row m of row tile rt is position j0 + 16 rt + m, so out = x W^T
 // leaves 4 consecutive keys of one head in a lane: one 16-byte store per head and tile.
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "kernels.h"
@@ -25,7 +28,7 @@ constexpr int K = rowstep::C;          // pair channels
 constexpr int MAX_HEADS = 384;         // LDS rows of the projection weight
 constexpr float kLog2eF = 1.4426950408889634f;
 
-template <typename TIN>
+template <typename TIN, typename TOUT>
 __global__ __launch_bounds__(512, 1) void pair_bias_kernel(PairBiasArgs a) {
   __shared__ __attribute__((aligned(16))) bf16 w_lds[MAX_HEADS * K];
   __shared__ __attribute__((aligned(16))) float lnw[K], lnb[K];
@@ -82,12 +85,20 @@ __global__ __launch_bounds__(512, 1) void pair_bias_kernel(PairBiasArgs a) {
 #pragma unroll
       for (int rt = 0; rt < 2; ++rt) {
         const int jb = j0 + 16 * rt + 4 * g;        // keys jb .. jb + 3
-        float4 v;
-        v.x = jb + 0 < n ? acc[rt][0] * kLog2eF : 0.f;
-        v.y = jb + 1 < n ? acc[rt][1] * kLog2eF : 0.f;
-        v.z = jb + 2 < n ? acc[rt][2] * kLog2eF : 0.f;
-        v.w = jb + 3 < n ? acc[rt][3] * kLog2eF : 0.f;
-        *reinterpret_cast<float4 *>(a.packed + (int64_t(h) * n + i) * npad + jb) = v;
+        const int64_t off = (int64_t(h) * n + i) * npad + jb;
+        if constexpr (std::is_same<TOUT, float>::value) {
+          float4 v;
+          v.x = jb + 0 < n ? acc[rt][0] * kLog2eF : 0.f;
+          v.y = jb + 1 < n ? acc[rt][1] * kLog2eF : 0.f;
+          v.z = jb + 2 < n ? acc[rt][2] * kLog2eF : 0.f;
+          v.w = jb + 3 < n ? acc[rt][3] * kLog2eF : 0.f;
+          *reinterpret_cast<float4 *>(static_cast<float *>(a.packed) + off) = v;
+        } else {
+          bf16x4 v;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = bf16(jb + e < n ? acc[rt][e] : 0.f);
+          *reinterpret_cast<bf16x4 *>(static_cast<bf16 *>(a.packed) + off) = v;
+        }
       }
     }
     cur = next;
@@ -107,10 +118,13 @@ int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s) {
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
   KernelTimer timer("pair_bias", s);
-  if (pair_dtype == XFH_BF16)
-    pair_bias_kernel<bf16><<<grid, 512, 0, s>>>(a);
-  else
-    pair_bias_kernel<float><<<grid, 512, 0, s>>>(a);
+  if (pair_dtype == XFH_BF16) {
+    if (a.packed_bf16) pair_bias_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
+    else pair_bias_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
+  } else {
+    if (a.packed_bf16) pair_bias_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
+    else pair_bias_kernel<float, float><<<grid, 512, 0, s>>>(a);
+  }
   return check_launch("pair_bias");
 }
 

@@ -31,7 +31,8 @@ LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so
 ABI_VERSION = 8
 
 F32, BF16, BOOL = 0, 1, 2
-BIAS_PACKED = 3                 # bias 'dtype' of a block written by xfh_attention_bias_pack
+BIAS_PACKED = 3                 # bias 'dtype' of a packed fp32 block (times log2(e))
+BIAS_PACKED_BF16 = 4            # bias 'dtype' of a packed bf16 block (natural units)
 EPI_STORE, EPI_MUL_SIGMOID_AUX, EPI_SIGMOID_MUL_AUX, EPI_ACCUMULATE, EPI_MUL_SIGMOID_AUX_ACCUMULATE = range(5)
 
 _p, _i, _i64, _f = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
@@ -58,8 +59,8 @@ SIGNATURES = {
     "xfh_attention_operands_size": (_i, [_i64, _i64, _i64, _i64, _pi64]),
     "xfh_attention_project": (_i, [_p, _i64, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _p, _p, _p, _p, _p]),
     "xfh_attention_mask_words": (_i, [_p, _i, _i64, _i64, _i64, _p, _p]),
-    "xfh_attention_operands": (_i, [_p, _p, _p, _p, _i, _p, _p, _p, _i64, _i64, _i64, _i64, _p]),
-    "xfh_pair_attention_bias": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _i64, _p, _p]),
+    "xfh_attention_operands": (_i, [_p, _p, _p, _p, _i, _p, _i, _p, _p, _i64, _i64, _i64, _i64, _p]),
+    "xfh_pair_attention_bias": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _i64, _p, _i, _p]),
     "xfh_triangle_multiplication_workspace_size": (_i64, [_i64, _i64, _i]),
     "xfh_triangle_multiplication": (_i, [_p, _i, _p, _i, _i64, _i64, _i, _p, _p, _f, _p, _p, _p, _p,
                                          _f, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
@@ -177,12 +178,27 @@ def compute_dtype(x: torch.Tensor, *weights: torch.Tensor) -> torch.dtype:
     return dtype
 
 
+def check_module(module: torch.nn.Module) -> None:
+    """Inference-only guard for a module's parameters (reference ``native.py:21-28``): a
+    parameter that requires grad matters only in grad mode, so the walk over them happens
+    only then; their device is checked where their pointers are taken (:func:`ptr`)."""
+    if torch.is_grad_enabled():
+        check_gpu_inference(*module.parameters())
+
+
 def ptr(tensor: Optional[torch.Tensor]) -> Optional[int]:
-    return None if tensor is None else tensor.data_ptr()
+    """Device address of a tensor handed to the library; a host tensor is refused here."""
+    if tensor is None:
+        return None
+    if not tensor.is_cuda:
+        raise ValueError("The 'hip' backend requires strided ROCm (cuda) tensors.")
+    return tensor.data_ptr()
 
 
 def stream_of(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The current stream of ``device`` as a raw hipStream_t."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def workspace(nbytes: int, device: torch.device) -> torch.Tensor:
@@ -226,8 +242,7 @@ class HipWeightCache:
         except RuntimeError:
             self.clear()
             return _prepare(weight, dtype, layout)
-        key = (weight.data_ptr(), version, tuple(weight.shape), tuple(weight.stride()),
-               weight.dtype, weight.device, dtype, layout)
+        key = (weight.data_ptr(), version, weight.shape, weight.stride(), weight.dtype, weight.device, dtype, layout)
         if self._key != key:
             self._value = _prepare(weight, dtype, layout)
             self._source = weight          # keeps the address from being reused
@@ -275,8 +290,8 @@ class FusedWeightCache:
 
     def get(self, weights, dtype: torch.dtype) -> torch.Tensor:
         try:
-            key = tuple((w.data_ptr(), w._version, tuple(w.shape), tuple(w.stride()), w.dtype,
-                         w.device) for w in weights) + (dtype,)
+            key = tuple((w.data_ptr(), w._version, w.shape, w.stride(), w.dtype, w.device)
+                        for w in weights) + (dtype,)
         except RuntimeError:
             self._key = self._sources = self._value = None
             return torch.cat([w.detach().to(dtype) for w in weights], dim=0).contiguous()
@@ -308,8 +323,7 @@ class DerivedWeightCache:
 
     def get(self, sources, build):
         try:
-            key = tuple((t.data_ptr(), t._version, tuple(t.shape), tuple(t.stride()), t.dtype, t.device)
-                        for t in sources)
+            key = tuple((t.data_ptr(), t._version, t.shape, t.stride(), t.dtype, t.device) for t in sources)
         except RuntimeError:
             self._key = self._sources = self._value = None
             return build(*sources)

@@ -152,13 +152,19 @@ def gated_linear_unit(x: torch.Tensor, packed: torch.Tensor, f: int, dtype: torc
 
 
 class PackedBias:
-    """One [H, Q, align64(K)] block of :func:`attention_bias_pack`'s output, passed to
-    :func:`attention` as its bias (the pipelined kernel reads it as it stands)."""
+    """One [H, Q, align64(K)] block of a packed bias, passed to :func:`attention` as its
+    bias (the pipelined kernel reads it as it stands): fp32 times log2(e)
+    (:func:`attention_bias_pack`, :func:`pair_attention_bias` in fp32) or bf16 in natural
+    units (:func:`pair_attention_bias` in bf16)."""
 
     def __init__(self, tensor: torch.Tensor):
-        if tensor.dim() != 3 or tensor.dtype != torch.float32 or not tensor.is_contiguous():
-            raise ValueError("PackedBias wraps one contiguous fp32 [H, Q, align64(K)] block")
+        if tensor.dim() != 3 or tensor.dtype not in (torch.float32, torch.bfloat16) or not tensor.is_contiguous():
+            raise ValueError("PackedBias wraps one contiguous fp32/bf16 [H, Q, align64(K)] block")
         self.tensor = tensor
+
+    @property
+    def code(self) -> int:
+        return nh.BIAS_PACKED if self.tensor.dtype == torch.float32 else nh.BIAS_PACKED_BF16
 
 
 def attention_bias_pack(bias: torch.Tensor) -> torch.Tensor:
@@ -177,20 +183,23 @@ def attention_bias_pack(bias: torch.Tensor) -> torch.Tensor:
 
 
 def pair_attention_bias(pair: torch.Tensor, ln_w: Optional[torch.Tensor], ln_b: Optional[torch.Tensor],
-                        eps: float, weight: torch.Tensor, owner: Optional[torch.nn.Module] = None) -> torch.Tensor:
-    """Linear(LayerNorm(pair)) as attention biases, [heads, N, align64(N)] fp32 in the packed
-    layout (one :class:`PackedBias` per block of heads); weight [heads, 128] in bf16."""
+                        eps: float, weight: torch.Tensor, owner: Optional[torch.nn.Module] = None,
+                        out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """Linear(LayerNorm(pair)) as attention biases, [heads, N, align64(N)] in the packed
+    layout (one :class:`PackedBias` per block of heads): fp32 times log2(e) (the modules'
+    choice: unrounded logits), or bf16 logits (the dtype of the reference's autocast Linear
+    output, half the bytes); weight [heads, 128] bf16."""
     n = pair.shape[0]
     if pair.dim() != 3 or pair.shape[1] != n or weight.dtype != torch.bfloat16:
         raise ValueError("pair_attention_bias: pair [N, N, C] and a bf16 weight")
     pair_c = pair.contiguous()
     heads = weight.shape[0]
-    out = torch.empty((heads, n, (n + 63) // 64 * 64), dtype=torch.float32, device=pair.device)
+    out = torch.empty((heads, n, (n + 63) // 64 * 64), dtype=out_dtype, device=pair.device)
     w = _fp32(ln_w, owner, "ln_weight")
     b = _fp32(ln_b, owner, "ln_bias")
     nh.call("xfh_pair_attention_bias", nh.ptr(pair_c), nh.dtype_code(pair.dtype), n, pair.shape[2],
             nh.ptr(w), nh.ptr(b), float(eps), nh.ptr(weight.contiguous()), nh.BF16, heads, nh.ptr(out),
-            nh.stream_of(pair.device))
+            nh.dtype_code(out_dtype), nh.stream_of(pair.device))
     return out
 
 
@@ -271,8 +280,8 @@ def attention_on_operands(operands: AttentionOperands, bias: PackedBias, out: to
     if out.dtype != torch.bfloat16 or not out.is_contiguous() or out.numel() != B * T * H * Dh:
         raise ValueError("attention_on_operands: out must be a contiguous bf16 [B, T, H*Dh]")
     nh.call("xfh_attention_operands", nh.ptr(operands.q), nh.ptr(operands.k), nh.ptr(operands.vt),
-            nh.ptr(operands.words), int(operands.words_shared), nh.ptr(bias.tensor), nh.ptr(operands.gate),
-            nh.ptr(out), B, T, H, Dh, nh.stream_of(out.device))
+            nh.ptr(operands.words), int(operands.words_shared), nh.ptr(bias.tensor), bias.code,
+            nh.ptr(operands.gate), nh.ptr(out), B, T, H, Dh, nh.stream_of(out.device))
     return out
 
 
@@ -317,7 +326,7 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, mask: Optional[
     if isinstance(bias, PackedBias):
         if tuple(bias.tensor.shape) != (H, Q, (K + 63) // 64 * 64):
             raise ValueError("attention: packed bias does not match [H, Q, align64(K)]")
-        bias_t, bias_code = bias.tensor, nh.BIAS_PACKED
+        bias_t, bias_code = bias.tensor, bias.code
     elif bias is not None:
         if bias.dtype not in (torch.float32, torch.bfloat16):
             bias = bias.to(torch.float32)

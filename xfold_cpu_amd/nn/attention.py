@@ -22,7 +22,8 @@ def grid_self_attention_hip(module: nn.Module, pair: torch.Tensor, mask: Optiona
     """``GridSelfAttention.forward`` (``xfold/nn/attention.py:80-105``): bias from the
     normalised, un-transposed pair; ending node (``transpose=True``) attends along the
     first axis with the mask unchanged; the result is in pair layout."""
-    nh.check_gpu_inference(pair, mask, *module.parameters())
+    nh.check_gpu_inference(pair, mask)
+    nh.check_module(module)
     dtype = nh.compute_dtype(pair, *(getattr(module, n).weight for n in _GRID_WEIGHTS))
     if pair.dim() != 3 or pair.shape[0] != pair.shape[1] or pair.shape[2] != module.c_pair:
         raise ValueError("GridSelfAttention expects pair [N, N, c_pair].")
@@ -82,7 +83,8 @@ def msa_attention_hip(module: nn.Module, msa: torch.Tensor, msa_mask: Optional[t
     msa_mask [S, N], pair [N, N, c_pair] -> [S, N, c_msa]. The attention weights come from
     the pair alone (with the key term ``1e9 * (max_s mask - 1)``) and are shared by every
     MSA row."""
-    nh.check_gpu_inference(msa, msa_mask, pair, *module.parameters())
+    nh.check_gpu_inference(msa, msa_mask, pair)
+    nh.check_module(module)
     dtype = nh.compute_dtype(msa, *(getattr(module, n).weight for n in _MSA_WEIGHTS))
     if msa.dim() != 3 or msa.shape[-1] != module.c_msa:
         raise ValueError("MSAAttention expects msa [S, N, c_msa].")

@@ -16,7 +16,8 @@ from ..fastnn import native_hip as nh
 def transition_hip(module: nn.Module, x: torch.Tensor,
                    accumulate_into: Optional[torch.Tensor] = None) -> torch.Tensor:
     """``transition2(GLU(LN(x), transition1.weight.T))`` (``xfold/nn/primitives.py:33-37``)."""
-    nh.check_gpu_inference(x, *module.parameters())
+    nh.check_gpu_inference(x)
+    nh.check_module(module)
     dtype = nh.compute_dtype(x, module.transition1.weight, module.transition2.weight)
     c = x.shape[-1]
     f = module.transition2.weight.shape[1]
@@ -74,7 +75,8 @@ def outer_product_mean_hip(module: nn.Module, msa: torch.Tensor, mask: torch.Ten
     mask [S, N] -> [N, N, num_output_channel]; the left x right outer product summed over
     the S sequences, projected by ``output_w``, plus ``output_b``, divided by
     ``epsilon + sum_s mask[s, i] mask[s, j]``."""
-    nh.check_gpu_inference(msa, mask, *module.parameters())
+    nh.check_gpu_inference(msa, mask)
+    nh.check_module(module)
     dtype = nh.compute_dtype(msa, module.left_projection.weight, module.right_projection.weight)
     if msa.dim() != 3 or msa.shape[-1] != module.c_msa:
         raise ValueError("OuterProductMean expects msa [S, N, c_msa].")

@@ -23,7 +23,8 @@ def triangle_multiplication_hip(module: nn.Module, pair: torch.Tensor, mask: Opt
     """Update of ``xfold/nn/triangle_multiplication.py:71-105`` (or ``pair += update`` in
     place when ``accumulate_into`` is the contiguous pair tensor itself)."""
     names = ("projection", "gate", "output_projection", "gating_linear")
-    nh.check_gpu_inference(pair, mask, *module.parameters())
+    nh.check_gpu_inference(pair, mask)
+    nh.check_module(module)
     dtype = nh.compute_dtype(pair, *(getattr(module, n).weight for n in names))
     if pair.dim() != 3 or pair.shape[0] != pair.shape[1] or pair.shape[2] != module.c_pair:
         raise ValueError("TriangleMultiplication expects pair [N, N, c_pair].")
