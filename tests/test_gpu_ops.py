@@ -572,12 +572,16 @@ def test_attention_operands_reused(device):
     assert vt[:, :, 24:].abs().max().item() == 0
 
 
-def test_attention_project_layouts(device):
+@pytest.mark.parametrize("B,T,H,Dh,K", [
+    (2, 45, 4, 20, 64),   # V columns share tiles with k / gate: element stores
+    (2, 48, 4, 16, 64),   # whole V tiles, T % 4 == 0: V^T from the swapped-operand MFMA
+    (3, 64, 2, 32, 96),
+])
+def test_attention_project_layouts(device, B, T, H, Dh, K):
     """xfh_attention_project's layouts against the stacked projection computed by a plain
     GEMM: q = (x Wq^T + b) * qscale, k, v^T (keys permuted inside runs of 32) and the gate,
     at the bf16 bar (the layouts hold the bf16-rounded products)."""
-    announce("attention project layouts")
-    B, T, H, Dh, K = 2, 45, 4, 20, 64
+    announce("attention project layouts", B, T, H, Dh, K)
     c = H * Dh
     g = torch.Generator().manual_seed(5)
     x = torch.randn(B * T, K, generator=g).bfloat16().to(device)
@@ -595,6 +599,11 @@ def test_attention_project_layouts(device):
     vt = ops_.vt.view(B, H, ops_.dp, ops_.tpad)[:, :, :Dh].float()[..., pos.to(device)]
     assert_parity(vt, parts[:, :, 2].permute(0, 2, 3, 1), TOL_BF16, "v^T layout")
     assert_parity(ops_.gate.float(), parts[:, :, 3].reshape(B, T, c), TOL_BF16, "gate layout")
+    # The padding stays zero: head-dim rows >= Dh, and the positions of keys >= T.
+    vt_all = ops_.vt.view(B, H, ops_.dp, ops_.tpad)
+    assert Dh == ops_.dp or vt_all[:, :, Dh:].abs().max().item() == 0
+    pad_pos = [(t & ~31) + ((t & 15) >> 2) * 8 + ((t & 31) >> 4) * 4 + (t & 3) for t in range(T, ops_.tpad)]
+    assert not pad_pos or vt_all[..., pad_pos].abs().max().item() == 0
 
 
 @pytest.mark.parametrize("bf16", [False, True])

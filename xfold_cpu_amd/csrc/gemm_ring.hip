@@ -218,6 +218,36 @@ __device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)
   }
 }
 
+// V^T tiles of an attention projection computed with swapped MFMA operands (acc[x][y][e] =
+// C[mw + y*16 + grp*4 + e][nw + x*16 + col]): keys t0 .. t0+3 of one head-dim row sit at 4
+// consecutive V^T positions (t0 % 4 == 0), one 8-byte store each.
+template <int NT>
+__device__ __forceinline__ void store_attn_vt(const GemmArgs &p, const f32x4 (&acc)[NT][4], int mw, int nw, int col,
+                                              int grp) {
+  const AttnOut &o = p.attn;
+  const int c = o.H * o.Dh;
+  int smp[4], pos[4];
+#pragma unroll
+  for (int y = 0; y < 4; ++y) {
+    const int t0 = mw + y * 16 + grp * 4;
+    smp[y] = t0 / o.T;
+    pos[y] = vt_position(t0 - smp[y] * o.T);
+  }
+#pragma unroll
+  for (int x = 0; x < NT; ++x) {
+    const int n = nw + x * 16 + col, w = n - 2 * c, h = w / o.Dh, d = w - h * o.Dh;
+    const float bias = p.bias ? p.bias[n] : 0.f;
+#pragma unroll
+    for (int y = 0; y < 4; ++y) {
+      if (mw + y * 16 + grp * 4 >= p.M) continue;   // M = B*T is a multiple of 4 here
+      bf16x4 v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) v[e] = bf16(acc[x][y][e] + bias);
+      *reinterpret_cast<bf16x4 *>(o.vt + ((int64_t(smp[y]) * o.H + h) * o.Dp + d) * o.Tpad + pos[y]) = v;
+    }
+  }
+}
+
 template <class G, int N> __device__ __forceinline__ void wait_younger(int younger) {
   // Waits until at most `younger` k-steps of this wavefront's loads are in flight.
   if constexpr (N == 0) {
@@ -297,27 +327,50 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
 #pragma unroll
   for (int s = 0; s < SLOTS - 1; ++s)
     if (s < steps) issue(s, s);
-  for (int s = 0; s < steps; ++s) {
-    // This wavefront's loads of step s have landed (the younger steps may still fly), then
-    // every wavefront's have, and every wavefront is done with step s - 1.
-    const int younger = steps - 1 - s;
-    wait_younger<G, SLOTS - 2>(younger);
-    __syncthreads();
-    if (s + SLOTS - 1 < steps) issue(s + SLOTS - 1, (s + SLOTS - 1) % SLOTS);
-    const bf16 *ta = lds + (s % SLOTS) * G::SLOT_ELEMS, *tb = ta + BM * TK;
+  // TR swaps the MFMA operands: acc[x][y][e] then holds C[m = .. + y*16 + grp*4 + e][n = ..
+  // + x*16 + col], four consecutive rows of one column (the V^T tiles of an attention
+  // projection, stored as 4 consecutive keys of one head-dim row).
+  auto main_loop = [&](auto tr_c) {
+    constexpr bool TR = decltype(tr_c)::value;
+    for (int s = 0; s < steps; ++s) {
+      // This wavefront's loads of step s have landed (the younger steps may still fly), then
+      // every wavefront's have, and every wavefront is done with step s - 1.
+      const int younger = steps - 1 - s;
+      wait_younger<G, SLOTS - 2>(younger);
+      __syncthreads();
+      if (s + SLOTS - 1 < steps) issue(s + SLOTS - 1, (s + SLOTS - 1) % SLOTS);
+      const bf16 *ta = lds + (s % SLOTS) * G::SLOT_ELEMS, *tb = ta + BM * TK;
 #pragma unroll
-    for (int ks = 0; ks < G::KS; ++ks) {
-      bf16x8 fa[4], fb[NT];
+      for (int ks = 0; ks < G::KS; ++ks) {
+        bf16x8 fa[4], fb[NT];
 #pragma unroll
-      for (int y = 0; y < 4; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * 64 + y * 16) * TK + frag[ks]);
+        for (int y = 0; y < 4; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * 64 + y * 16) * TK + frag[ks]);
 #pragma unroll
-      for (int x = 0; x < NT; ++x) {
-        fb[x] = *reinterpret_cast<const bf16x8 *>(tb + (wn * WN + x * 16) * TK + frag[ks]);
+        for (int x = 0; x < NT; ++x) {
+          fb[x] = *reinterpret_cast<const bf16x8 *>(tb + (wn * WN + x * 16) * TK + frag[ks]);
 #pragma unroll
-        for (int y = 0; y < 4; ++y) acc[x][y] = mfma16(fb[x], fa[y], acc[x][y]);
+          for (int y = 0; y < 4; ++y)
+            acc[x][y] = TR ? mfma16(fa[y], fb[x], acc[x][y]) : mfma16(fb[x], fa[y], acc[x][y]);
+        }
       }
     }
+  };
+  constexpr bool kAttnOut = !GLU && std::is_same<TO, bf16>::value;
+  bool vt_tile = false;
+  if constexpr (kAttnOut) {
+    // A workgroup whose columns all fall in the V part writes V^T in 8-byte key runs when
+    // groups of 4 rows never straddle two samples (T % 4 == 0).
+    const int c = p.attn.H * p.attn.Dh;
+    vt_tile = p.attn.q && p.attn.T % 4 == 0 && n0 >= 2 * c && n0 + BN <= 3 * c;
   }
+  if (vt_tile) {
+    if constexpr (kAttnOut) {
+      main_loop(std::true_type{});
+      store_attn_vt<NT>(p, acc, m0 + wm * 64, n0 + wn * WN, col, grp);
+    }
+    return;
+  }
+  main_loop(std::false_type{});
 
   // acc[x][y][e] = C[m = m0 + wm*64 + y*16 + col][n = n0 + wn*WN + x*16 + grp*4 + e]
   TO *C = static_cast<TO *>(p.C) + batch * p.sC;
