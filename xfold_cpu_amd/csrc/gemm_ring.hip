@@ -258,7 +258,8 @@ template <class G, int N> __device__ __forceinline__ void wait_younger(int young
   }
 }
 
-template <typename TO, bool GLU, class G, bool XCD = false>
+// ATTN: the attention-operand output (AttnOut, bf16, store epilogue) instead of C.
+template <typename TO, bool GLU, class G, bool XCD = false, bool ATTN = false>
 __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
   constexpr int BM = G::BM, BN = G::BN, TK = G::TK, SLOTS = G::SLOTS, CH = G::CH, NT = G::NT;
   constexpr int RPP = G::ROWS_PER_PIECE, PPW = G::PPW, WN = BN / 2;
@@ -355,13 +356,14 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
       }
     }
   };
-  constexpr bool kAttnOut = !GLU && std::is_same<TO, bf16>::value;
+  static_assert(!ATTN || (!GLU && std::is_same<TO, bf16>::value), "attention output: bf16 store only");
+  constexpr bool kAttnOut = ATTN;
   bool vt_tile = false;
   if constexpr (kAttnOut) {
     // A workgroup whose columns all fall in the V part writes V^T in 8-byte key runs when
     // groups of 4 rows never straddle two samples (T % 4 == 0).
     const int c = p.attn.H * p.attn.Dh;
-    vt_tile = p.attn.q && p.attn.T % 4 == 0 && n0 >= 2 * c && n0 + BN <= 3 * c;
+    vt_tile = p.attn.T % 4 == 0 && n0 >= 2 * c && n0 + BN <= 3 * c;
   }
   if (vt_tile) {
     if constexpr (kAttnOut) {
@@ -401,11 +403,9 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     return;
   }
   const int mw = m0 + wm * 64, nw = n0 + wn * WN;
-  if constexpr (std::is_same<TO, bf16>::value) {
-    if (p.attn.q) {
-      store_attn<NT>(p, acc, mw, nw, col, grp);
-      return;
-    }
+  if constexpr (ATTN) {
+    store_attn<NT>(p, acc, mw, nw, col, grp);
+    return;
   }
   switch (p.epi) {
     case XFH_EPI_MUL_SIGMOID_AUX:
@@ -457,6 +457,10 @@ template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dty
     } else {
       return fail(XFH_EUNSUPPORTED, "gemm_ring: GLU needs whole 32-column groups per wavefront");
     }
+  } else if (p.attn.q) {
+    if (out_dtype != XFH_BF16) return fail(XFH_EUNSUPPORTED, "gemm_ring: the attention layouts are bf16");
+    if (p.xcd_split) gemm_ring_kernel<bf16, false, G, true, true><<<grid, 256, 0, s>>>(p);
+    else gemm_ring_kernel<bf16, false, G, false, true><<<grid, 256, 0, s>>>(p);
   } else if (p.xcd_split) {
     if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, false, G, true><<<grid, 256, 0, s>>>(p);
     else gemm_ring_kernel<float, false, G, true><<<grid, 256, 0, s>>>(p);
