@@ -2,8 +2,8 @@
 // the projections and transitions (k a multiple of 32, 16-byte aligned rows). Same contract
 // as gemm_nt (gemm.hip), which keeps every other case.
 //
-// Tiling: 128 x BN output tile per workgroup (BN = 64, 96 or 128), 4 wavefronts in a 2 x 2
-// grid each owning 64 x BN/2 (4 x BN/32 MFMA 16x16x32 tiles). Per k-step of TK (32 or 64)
+// Tiling: BM x BN output tile per workgroup (BM = 128 or 256, BN = 64 .. 192), 4 wavefronts
+// in a 2 x 2 grid each owning BM/2 x BN/2 (BM/32 x BN/32 MFMA 16x16x32 tiles). Per k-step of TK (32 or 64)
 // both operand tiles go global -> LDS with direct loads (global_load_lds_dwordx4, no
 // registers) into a ring of SLOTS stages: the loads of steps s+1 .. s+SLOTS-1 are in
 // flight while step s is multiplied, one barrier per step. A TK-deep row is CH = TK/8
@@ -27,8 +27,10 @@ namespace {
 typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
-template <int BN_, int TK_, int SLOTS_, int WGS_> struct Ring {
-  static constexpr int BM = 128, BN = BN_, TK = TK_, SLOTS = SLOTS_, WGS = WGS_;
+template <int BN_, int TK_, int SLOTS_, int WGS_, int BM_ = 128> struct Ring {
+  static constexpr int BM = BM_, BN = BN_, TK = TK_, SLOTS = SLOTS_, WGS = WGS_;
+  static constexpr int WM = BM / 2;                   // rows per wavefront (2 x 2 wavefront grid)
+  static constexpr int MT = WM / 16;                  // MFMA tiles per wavefront along m
   static constexpr int CH = TK / 8;                   // 16-byte chunks per LDS row
   static constexpr int ROWS_PER_PIECE = 1024 / (2 * TK);   // rows per 1 KB direct load
   static constexpr int PIECES = (BM + BN) / ROWS_PER_PIECE; // per k-step
@@ -82,18 +84,18 @@ template <int EPI> __device__ __forceinline__ float epilogue(float acc, float c,
 // quantities (row divisor, auxiliary row) are taken once per row: a runtime switch per
 // element made this code ~10x larger than the main loop, and its instruction-cache misses
 // cost ~10 us per launch whatever the grid.
-template <int EPI, typename TO, int NT>
-__device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)[NT][4], int64_t batch, int mw,
+template <int EPI, typename TO, int NT, int MT>
+__device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)[NT][MT], int64_t batch, int mw,
                                            int nw, int col, int grp) {
   constexpr bool READS_C = EPI == XFH_EPI_ACCUMULATE || EPI == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
   constexpr bool AUX = EPI == XFH_EPI_MUL_SIGMOID_AUX || EPI == XFH_EPI_SIGMOID_MUL_AUX ||
                        EPI == XFH_EPI_MUL_SIGMOID_AUX_ACCUMULATE;
   TO *C = static_cast<TO *>(p.C) + batch * p.sC;
-  int m[4];
-  float rs[4];
-  const TO *arow[4];
+  int m[MT];
+  float rs[MT];
+  const TO *arow[MT];
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
+  for (int y = 0; y < MT; ++y) {
     m[y] = mw + y * 16 + col;
     rs[y] = p.row_div && m[y] < p.M ? 1.0f / (p.row_div_eps + p.row_div[m[y]]) : 1.0f;
     arow[y] = nullptr;
@@ -102,7 +104,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)
       arow[y] = static_cast<const TO *>(p.aux) + batch * p.sAux + int64_t(ar) * p.ldaux;
     }
   }
-  if (p.pair_blk == 0 && mw + 64 <= p.M && nw + 16 * NT <= p.N) {
+  if (p.pair_blk == 0 && mw + 16 * MT <= p.M && nw + 16 * NT <= p.N) {
     // Interior sub-tile (every tile of the usual shapes): straight-line code, no per-element
     // bounds, row-major addresses.
 #pragma unroll
@@ -113,7 +115,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)
 #pragma unroll
         for (int e = 0; e < 4; ++e) bias[e] = p.bias[batch * p.sBias + n + e];
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
+      for (int y = 0; y < MT; ++y) {
         TO *c = C + int64_t(m[y]) * p.ldc + n;
         float cv[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f}, out[4];
         if constexpr (READS_C) Vec4<TO>::load(c, cv);
@@ -135,7 +137,7 @@ __device__ __forceinline__ void store_tile(const GemmArgs &p, const f32x4 (&acc)
 #pragma unroll
       for (int e = 0; e < 4; ++e) bias[e] = n + e < p.N ? p.bias[batch * p.sBias + n + e] : 0.f;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
+    for (int y = 0; y < MT; ++y) {
       if (m[y] >= p.M) continue;
       TO *c = c_element(p, C, m[y], n);
       float cv[4] = {0.f, 0.f, 0.f, 0.f}, av[4] = {0.f, 0.f, 0.f, 0.f}, out[4];
@@ -174,14 +176,14 @@ __device__ __forceinline__ int vt_position(int t) {
 // Store epilogue into the attention-operand layouts (AttnOut): (acc + bias), times qscale
 // for the q columns. Four consecutive columns share one part and head (Dh % 4 == 0): q, k
 // and gate take one 8-byte store, V^T four 2-byte stores (one per head-dim row).
-template <int NT>
-__device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)[NT][4], int mw, int nw, int col,
+template <int NT, int MT>
+__device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)[NT][MT], int mw, int nw, int col,
                                            int grp) {
   const AttnOut &o = p.attn;
   const int c = o.H * o.Dh;
-  int smp[4], tok[4];                                 // per row: sample b and token t
+  int smp[MT], tok[MT];                                 // per row: sample b and token t
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
+  for (int y = 0; y < MT; ++y) {
     const int m = mw + y * 16 + col;
     smp[y] = m / o.T;
     tok[y] = m - smp[y] * o.T;
@@ -197,7 +199,7 @@ __device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)
 #pragma unroll
       for (int e = 0; e < 4; ++e) bias[e] = p.bias[n + e];
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
+    for (int y = 0; y < MT; ++y) {
       if (mw + y * 16 + col >= p.M) continue;
       bf16x4 v;
 #pragma unroll
@@ -221,14 +223,14 @@ __device__ __forceinline__ void store_attn(const GemmArgs &p, const f32x4 (&acc)
 // V^T tiles of an attention projection computed with swapped MFMA operands (acc[x][y][e] =
 // C[mw + y*16 + grp*4 + e][nw + x*16 + col]): keys t0 .. t0+3 of one head-dim row sit at 4
 // consecutive V^T positions (t0 % 4 == 0), one 8-byte store each.
-template <int NT>
-__device__ __forceinline__ void store_attn_vt(const GemmArgs &p, const f32x4 (&acc)[NT][4], int mw, int nw, int col,
+template <int NT, int MT>
+__device__ __forceinline__ void store_attn_vt(const GemmArgs &p, const f32x4 (&acc)[NT][MT], int mw, int nw, int col,
                                               int grp) {
   const AttnOut &o = p.attn;
   const int c = o.H * o.Dh;
-  int smp[4], pos[4];
+  int smp[MT], pos[MT];
 #pragma unroll
-  for (int y = 0; y < 4; ++y) {
+  for (int y = 0; y < MT; ++y) {
     const int t0 = mw + y * 16 + grp * 4;
     smp[y] = t0 / o.T;
     pos[y] = vt_position(t0 - smp[y] * o.T);
@@ -238,7 +240,7 @@ __device__ __forceinline__ void store_attn_vt(const GemmArgs &p, const f32x4 (&a
     const int n = nw + x * 16 + col, w = n - 2 * c, h = w / o.Dh, d = w - h * o.Dh;
     const float bias = p.bias ? p.bias[n] : 0.f;
 #pragma unroll
-    for (int y = 0; y < 4; ++y) {
+    for (int y = 0; y < MT; ++y) {
       if (mw + y * 16 + grp * 4 >= p.M) continue;   // M = B*T is a multiple of 4 here
       bf16x4 v;
 #pragma unroll
@@ -262,7 +264,7 @@ template <class G, int N> __device__ __forceinline__ void wait_younger(int young
 template <typename TO, bool GLU, class G, bool XCD = false, bool ATTN = false>
 __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
   constexpr int BM = G::BM, BN = G::BN, TK = G::TK, SLOTS = G::SLOTS, CH = G::CH, NT = G::NT;
-  constexpr int RPP = G::ROWS_PER_PIECE, PPW = G::PPW, WN = BN / 2;
+  constexpr int RPP = G::ROWS_PER_PIECE, PPW = G::PPW, WN = BN / 2, WM = G::WM, MT = G::MT;
   __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * G::SLOT_ELEMS];
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave >> 1, wn = wave & 1, col = lane & 15, grp = lane >> 4;
@@ -318,11 +320,11 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
 #pragma unroll
   for (int ks = 0; ks < G::KS; ++ks) frag[ks] = col * TK + ((4 * ks + grp) ^ G::sw(col)) * 8;
 
-  f32x4 acc[NT][4];   // [x][y]: rows n (A operand = B rows), cols m (B operand = A rows)
+  f32x4 acc[NT][MT];   // [x][y]: rows n (A operand = B rows), cols m (B operand = A rows)
 #pragma unroll
   for (int x = 0; x < NT; ++x)
 #pragma unroll
-    for (int y = 0; y < 4; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int y = 0; y < MT; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   const int steps = p.K / TK;
 #pragma unroll
@@ -343,14 +345,14 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
       const bf16 *ta = lds + (s % SLOTS) * G::SLOT_ELEMS, *tb = ta + BM * TK;
 #pragma unroll
       for (int ks = 0; ks < G::KS; ++ks) {
-        bf16x8 fa[4], fb[NT];
+        bf16x8 fa[MT], fb[NT];
 #pragma unroll
-        for (int y = 0; y < 4; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * 64 + y * 16) * TK + frag[ks]);
+        for (int y = 0; y < MT; ++y) fa[y] = *reinterpret_cast<const bf16x8 *>(ta + (wm * WM + y * 16) * TK + frag[ks]);
 #pragma unroll
         for (int x = 0; x < NT; ++x) {
           fb[x] = *reinterpret_cast<const bf16x8 *>(tb + (wn * WN + x * 16) * TK + frag[ks]);
 #pragma unroll
-          for (int y = 0; y < 4; ++y)
+          for (int y = 0; y < MT; ++y)
             acc[x][y] = TR ? mfma16(fa[y], fb[x], acc[x][y]) : mfma16(fb[x], fa[y], acc[x][y]);
         }
       }
@@ -368,13 +370,13 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
   if (vt_tile) {
     if constexpr (kAttnOut) {
       main_loop(std::true_type{});
-      store_attn_vt<NT>(p, acc, m0 + wm * 64, n0 + wn * WN, col, grp);
+      store_attn_vt(p, acc, m0 + wm * WM, n0 + wn * WN, col, grp);
     }
     return;
   }
   main_loop(std::false_type{});
 
-  // acc[x][y][e] = C[m = m0 + wm*64 + y*16 + col][n = n0 + wn*WN + x*16 + grp*4 + e]
+  // acc[x][y][e] = C[m = m0 + wm*WM + y*16 + col][n = n0 + wn*WN + x*16 + grp*4 + e]
   TO *C = static_cast<TO *>(p.C) + batch * p.sC;
   if constexpr (GLU) {
     // Packed GLU weight: 32-column groups = 16 gate columns then the 16 matching value
@@ -384,8 +386,8 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     for (int q = 0; q < NT / 2; ++q) {
       const int f = (n0 + wn * WN) / 2 + q * 16 + grp * 4;
 #pragma unroll
-      for (int y = 0; y < 4; ++y) {
-        const int m = m0 + wm * 64 + y * 16 + col;
+      for (int y = 0; y < MT; ++y) {
+        const int m = m0 + wm * WM + y * 16 + col;
         if (m >= p.M) continue;
         float v[4];
 #pragma unroll
@@ -402,9 +404,9 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
     }
     return;
   }
-  const int mw = m0 + wm * 64, nw = n0 + wn * WN;
+  const int mw = m0 + wm * WM, nw = n0 + wn * WN;
   if constexpr (ATTN) {
-    store_attn<NT>(p, acc, mw, nw, col, grp);
+    store_attn(p, acc, mw, nw, col, grp);
     return;
   }
   switch (p.epi) {
