@@ -1,6 +1,7 @@
 """Benchmark of the HIP Pairformer path on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--gpus 1] [--config C2] [--no-cpu-baseline] [--no-c3]
+                    [--no-cached] [--graph]
 
 A step is one forward pass of the configured workload over synthetic inputs already in
 HBM: C2 (default, the metric's N=384 configuration) = one Pairformer pair block at N=384
@@ -48,6 +49,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-c3", action="store_true",
                    help="with the default C2 configuration, skip the 48-block C3 trunk timed beside it")
+    p.add_argument("--no-cached", action="store_true",
+                   help="with C4, skip the input-cache forward timed beside the uncached one")
     p.add_argument("--graph", action="store_true",
                    help="capture one step in a HIP graph after the warm-up and time its replays")
     p.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -400,7 +403,7 @@ def main():
     # The north-star target (C3, the 48-block trunk at N=768) is timed beside the metric's
     # N=384 configuration in the default run.
     extra = {}
-    if args.config == "C4":
+    if args.config == "C4" and not args.no_cached:
         extra["cached_forward_ms"] = round(time_cached_diffusion(device, args.steps, max(1, args.warmup)), 4)
         log(f"C4 with the input cache: {extra['cached_forward_ms']} ms per forward")
     c3 = None

@@ -572,6 +572,41 @@ def test_attention_operands_reused(device):
     assert vt[:, :, 24:].abs().max().item() == 0
 
 
+def test_attention_operand_mask_words_follow_the_mask(device):
+    """The per-stream shared operand buffers recompute their kept-key words when the mask
+    changes in place, when another mask tensor comes (even one allocated after the first is
+    dropped) and for every inference-mode mask: each call equals one on fresh buffers."""
+    announce("attention operand mask words")
+    _, hip = pair_of("SelfAttention", dict(c_x=384, c_single_cond=64, num_head=16, use_single_cond=True), seed=4)
+    g = torch.Generator().manual_seed(4)
+    n = 96
+    x = torch.randn(2, n, 384, generator=g).bfloat16().to(device)
+    packed = ops.PackedBias(ops.attention_bias_pack(torch.randn(1, 16, n, n, generator=g).to(device))[0])
+    single = torch.randn(n, 64, generator=g).to(device)
+
+    def run(mask, fresh):
+        operands = ops.AttentionOperands(2, n, 16, 24, device) if fresh else None
+        with torch.no_grad(), autocast(True):
+            return hnn.self_attention_hip(hip, x, mask, packed, single, _operands=operands)
+    mask = torch.ones(n, device=device)
+    mask[-5:] = 0
+    first = run(mask, False)
+    assert torch.equal(first, run(mask, True))
+    mask[-30:] = 0                                    # in place: version bump
+    second = run(mask, False)
+    assert torch.equal(second, run(mask, True)) and not torch.equal(first, second)
+    del mask
+    other = torch.ones(n, device=device)
+    other[:7] = 0
+    third = run(other, False)
+    assert torch.equal(third, run(other, True))
+    with torch.inference_mode():
+        inf_mask = torch.ones(n, device=device)
+        inf_mask[10:20] = 0
+    fourth = run(inf_mask, False)
+    assert torch.equal(fourth, run(inf_mask, True)) and not torch.equal(third, fourth)
+
+
 @pytest.mark.parametrize("B,T,H,Dh,K", [
     (2, 45, 4, 20, 64),   # V columns share tiles with k / gate: element stores
     (2, 48, 4, 16, 64),   # whole V tiles, T % 4 == 0: V^T from the swapped-operand MFMA

@@ -8,7 +8,9 @@ library call on the current stream. None of them computes anything with torch.
 
 from __future__ import annotations
 
+import collections
 import ctypes
+import threading
 from typing import Optional
 
 import torch
@@ -223,6 +225,7 @@ class AttentionOperands:
         self.words = torch.empty(B * (self.tpad // 64), dtype=torch.int64, device=device)
         self.words_shared = True
         self._mask_key = ()
+        self._mask_ref = None
 
     @staticmethod
     def supported(T: int, H: int, Dh: int) -> bool:
@@ -234,8 +237,9 @@ class AttentionOperands:
     def set_mask(self, mask: Optional[torch.Tensor]) -> None:
         """Kept-key words of a key mask: None, [T] (shared by the samples) or [B, T]."""
         # Inference tensors carry no version counter: their words are recomputed every time.
+        # The mask of the cached words is held, so its address cannot pass to another tensor.
         key = (None,) if mask is None else \
-            None if mask.is_inference() else (mask.data_ptr(), mask._version, tuple(mask.shape), mask.dtype)
+            None if mask.is_inference() else (id(mask), mask.data_ptr(), mask._version, tuple(mask.shape), mask.dtype)
         if key is not None and key == self._mask_key:
             return
         B, T = self.shape[0], self.shape[1]
@@ -245,14 +249,36 @@ class AttentionOperands:
                 rows = B
             elif tuple(mask.shape) != (T,):
                 raise ValueError(f"attention operands: mask must be [{T}] or [{B}, {T}]")
-            if mask.dtype not in (torch.bool, torch.uint8, torch.float32, torch.bfloat16):
-                mask = mask.to(torch.bool)
-            m = mask.contiguous()
+            m = mask if mask.dtype in (torch.bool, torch.uint8, torch.float32, torch.bfloat16) else mask.to(torch.bool)
+            m = m.contiguous()
             code = nh.BOOL if m.dtype in (torch.bool, torch.uint8) else nh.dtype_code(m.dtype)
         nh.call("xfh_attention_mask_words", nh.ptr(m), code, T, rows, T, nh.ptr(self.words),
                 nh.stream_of(self.device))
         self.words_shared = rows == 1
         self._mask_key = key
+        self._mask_ref = mask
+
+
+_SHARED_OPERANDS: "collections.OrderedDict" = collections.OrderedDict()
+_SHARED_OPERANDS_MAX = 8
+
+
+def shared_attention_operands(B: int, T: int, H: int, Dh: int, device: torch.device) -> AttentionOperands:
+    """One :class:`AttentionOperands` set per (shape, device, current stream, thread), kept
+    between calls: work queued on one stream runs in order, so every attention call of that
+    stream can reuse the same buffers (zeroed once, padding never written) instead of
+    allocating and zero-filling its own. The least recently used of more than 8 sets is
+    released (the caching allocator keeps it from reuse until the queued work is done)."""
+    device = torch.device(device)
+    key = (B, T, H, Dh, device, nh.stream_of(device), threading.get_ident())
+    ops_ = _SHARED_OPERANDS.get(key)
+    if ops_ is None:
+        ops_ = _SHARED_OPERANDS[key] = AttentionOperands(B, T, H, Dh, device)
+        while len(_SHARED_OPERANDS) > _SHARED_OPERANDS_MAX:
+            _SHARED_OPERANDS.popitem(last=False)
+    else:
+        _SHARED_OPERANDS.move_to_end(key)
+    return ops_
 
 
 def attention_project(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor],

@@ -147,7 +147,7 @@ def self_attention_hip(module: nn.Module, x: torch.Tensor, mask: Optional[torch.
             (mask is None or tuple(mask.shape) in ((n,), (samples, n))):
         operands = _operands
         if operands is None or not operands.matches(samples, n, heads, d, x.device):
-            operands = ops.AttentionOperands(samples, n, heads, d, x.device)
+            operands = ops.shared_attention_operands(samples, n, heads, d, x.device)
         operands.set_mask(mask)
         w_all = nh.fused_linear_weight(module, _QKV + ("gating_query",), dtype)
         ops.attention_project(xn, w_all, _projection_bias(module, c, 4, x.device), operands, d ** -0.5 * _LOG2E)
@@ -255,15 +255,15 @@ def _cached(module: nn.Module, name: str, dependencies, factory, modules):
 
 
 def _block_operands(module: nn.Module, act: torch.Tensor, mask: Optional[torch.Tensor]):
-    """One set of attention-operand buffers (and mask words) for every block of a forward,
-    or None when the blocks' attention takes the general path."""
+    """The attention-operand buffers (and mask words) every block of a forward uses, or None
+    when the blocks' attention takes the general path."""
     samples = 1 if act.dim() == 2 else act.shape[0]
     n, c, heads = act.shape[-2], act.shape[-1], module.num_head
     if c % heads or not ops.AttentionOperands.supported(n, heads, c // heads):
         return None
     if mask is not None and tuple(mask.shape) not in ((n,), (samples, n)):
         return None
-    operands = ops.AttentionOperands(samples, n, heads, c // heads, act.device)
+    operands = ops.shared_attention_operands(samples, n, heads, c // heads, act.device)
     operands.set_mask(mask)
     return operands
 
