@@ -83,6 +83,13 @@ template <typename T> __device__ __forceinline__ T from_f32(float v) { return st
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
 
 // sigmoid / SiLU with the hardware reciprocal (1 ulp) instead of an IEEE division.
+// Workgroup barrier for rings of direct global->LDS loads: waits for this wavefront's LDS
+// operations only, then s_barrier. __syncthreads() also waits vmcnt(0), i.e. for every
+// direct load in flight, including those of the steps still ahead of the one about to be
+// read; the rings already wait, per wavefront, exactly for the loads of that step. The asm
+// has a memory clobber, so no LDS access moves across it.
+__device__ __forceinline__ void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 __device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 

@@ -94,18 +94,31 @@ __global__ __launch_bounds__(256, 2) void contraction_kernel(ContractionArgs a) 
     // then every wavefront's have, and every wavefront is done with step s-1.
     if (s + 1 < steps) asm volatile("s_waitcnt vmcnt(6)" ::: "memory");
     else asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    ring_barrier();
     if (s + 2 < steps) issue(s + 2, (s + 2) % SLOTS);
     const bf16 *tl = lds + (s % SLOTS) * SLOT_ELEMS, *tr = tl + OP_ELEMS;
+    // All L fragments and the first two R fragments, then each pair of R fragments is read
+    // while the previous pair's 12 MFMAs run (scheduling barriers keep the compiler from
+    // sinking the reads next to their use).
     bf16x8 fl[NT], fr[NT];
 #pragma unroll
     for (int y = 0; y < NT; ++y)
       fl[y] = *reinterpret_cast<const bf16x8 *>(tl + (wi * WT + y * 16) * TK + frag);
 #pragma unroll
-    for (int x = 0; x < NT; ++x) {
-      fr[x] = *reinterpret_cast<const bf16x8 *>(tr + (wj * WT + x * 16) * TK + frag);
+    for (int x = 0; x < 2; ++x) fr[x] = *reinterpret_cast<const bf16x8 *>(tr + (wj * WT + x * 16) * TK + frag);
 #pragma unroll
-      for (int y = 0; y < NT; ++y) acc[x][y] = mfma16(fr[x], fl[y], acc[x][y]);
+    for (int xp = 0; xp < NT / 2; ++xp) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (xp + 1 < NT / 2) {
+#pragma unroll
+        for (int x = 2 * xp + 2; x < 2 * xp + 4; ++x)
+          fr[x] = *reinterpret_cast<const bf16x8 *>(tr + (wj * WT + x * 16) * TK + frag);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int x = 2 * xp; x < 2 * xp + 2; ++x)
+#pragma unroll
+        for (int y = 0; y < NT; ++y) acc[x][y] = mfma16(fr[x], fl[y], acc[x][y]);
     }
   }
 

@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256, G::WGS) void gemm_ring_kernel(GemmArgs p) {
       // every wavefront's have, and every wavefront is done with step s - 1.
       const int younger = steps - 1 - s;
       wait_younger<G, SLOTS - 2>(younger);
-      __syncthreads();
+      ring_barrier();
       if (s + SLOTS - 1 < steps) issue(s + SLOTS - 1, (s + SLOTS - 1) % SLOTS);
       const bf16 *ta = lds + (s % SLOTS) * G::SLOT_ELEMS, *tb = ta + BM * TK;
 #pragma unroll

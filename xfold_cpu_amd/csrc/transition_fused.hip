@@ -193,7 +193,7 @@ __global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(Trans
       // then every wavefront's have, and every wavefront is done with chunk gc - 1.
       if (gc + 1 >= total_chunks) wait_vmcnt<0>();
       else wait_vmcnt<SEG_PER_WAVE>();
-      __syncthreads();
+      ring_barrier();
       if (gc + 2 < total_chunks) issue(gc + 2);
       if constexpr (NS == 0) continue;
       const bf16 *w1s = ring + (gc % SLOTS) * SLOT, *w2s = w1s + W1_STAGE;
