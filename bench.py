@@ -194,10 +194,14 @@ def kernel_roofline(step, n, steps):
     from xfold_cpu_amd.fastnn import native_hip
     from xfold_cpu_amd.kernel_bench import pair_kernel_work, rates
 
-    for name in PAIR_TIMERS:
-        native_hip.kernel_timing_read(name)           # drop anything recorded earlier
     native_hip.set_kernel_timing(True)
     try:
+        # One step with the timers on is dropped: the first event records of a process
+        # read up to 15% high on a fresh box.
+        step()
+        torch.cuda.synchronize()
+        for name in PAIR_TIMERS:
+            native_hip.kernel_timing_read(name)       # drop it and anything recorded earlier
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
@@ -377,7 +381,7 @@ def run_config(cfg_name, steps, warmup, device, graph=False):
     log(f"{cfg_name} timed {steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
     roof, kernels = None, None
     if cfg["kind"] != "diffusion":
-        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(steps, 5)))
+        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(steps, 10)))
         log(f"{cfg_name} roofline: {roof}")
     return dict(ms_step=ms_step, blocks=blocks, workload=workload, cfg=cfg, roofline=roof, kernels=kernels)
 
