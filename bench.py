@@ -202,6 +202,10 @@ def kernel_roofline(step, n, steps):
         torch.cuda.synchronize()
         for name in PAIR_TIMERS:
             native_hip.kernel_timing_read(name)       # drop it and anything recorded earlier
+        # A launch's start event is recorded when the GPU reaches it; if the host is still
+        # submitting the kernel then, the wait counts as kernel time. A ~10 ms spin kernel
+        # first lets the host queue the steps ahead of the GPU.
+        torch.cuda._sleep(20_000_000)
         for _ in range(steps):
             step()
         torch.cuda.synchronize()
