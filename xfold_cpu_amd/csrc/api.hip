@@ -62,15 +62,22 @@ KernelTimer::KernelTimer(const char *name, hipStream_t stream) : name_(name), st
   if (!g_timing_enabled) return;
   hipEvent_t e;
   if (hipEventCreate(&e) != hipSuccess) return;
-  hipEventRecord(e, stream_);
+  if (hipEventRecord(e, stream_) != hipSuccess) {   // untimed launch: no record is kept
+    (void)hipEventDestroy(e);
+    return;
+  }
   start_ = e;
 }
 
 KernelTimer::~KernelTimer() {
   if (!start_) return;
   hipEvent_t e;
-  if (hipEventCreate(&e) != hipSuccess) return;
-  hipEventRecord(e, stream_);
+  const bool created = hipEventCreate(&e) == hipSuccess;
+  if (!created || hipEventRecord(e, stream_) != hipSuccess) {
+    if (created) (void)hipEventDestroy(e);
+    (void)hipEventDestroy(static_cast<hipEvent_t>(start_));
+    return;
+  }
   std::lock_guard<std::mutex> lock(g_timing_mutex);
   g_timed.push_back({name_, static_cast<hipEvent_t>(start_), e});
 }
@@ -191,8 +198,8 @@ int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches
       return fail(XFH_EHIP, "kernel_timing_read: elapsed time failed");
     total += ms;
     ++count;
-    hipEventDestroy(t.start);
-    hipEventDestroy(t.stop);
+    (void)hipEventDestroy(t.start);
+    (void)hipEventDestroy(t.stop);
   }
   g_timed.swap(keep);
   *total_ms = total;
