@@ -110,3 +110,36 @@ def test_reset_input_cache_releases_module_caches():
         assert model[0]._input_cache._entries
         reset_input_cache(model)
         assert not model[0]._input_cache._entries
+
+
+def test_a_new_tensor_at_the_same_address_or_another_autocast_state_is_a_miss():
+    """Validity is the held object itself (not its id or address) with an unchanged
+    stamp, plus the autocast state and module settings the value was computed under."""
+    owner, cache, feature = nn.Linear(3, 3).eval(), InputCache(), torch.randn(2, 3)
+    calls = []
+
+    def factory():
+        calls.append(1)
+        return feature * 2
+    with torch.no_grad(), input_cache_scope() as scope:
+        cache.get("x", (feature, 4), owner, factory)
+        alias = feature.view(2, 3)                   # same storage and address, new object
+        cache.get("x", (alias, 4), owner, factory)
+        cache.get("x", (alias, 5), owner, factory)   # a non-tensor leaf changed
+        with torch.autocast("cpu", dtype=torch.bfloat16):
+            cache.get("x", (alias, 5), owner, factory)
+        assert len(calls) == 4
+        assert scope.used == feature.untyped_storage().nbytes()
+    assert scope.used == 0 and not cache._entries
+
+
+def test_entries_are_charged_per_distinct_storage():
+    owner, cache = nn.Linear(3, 3).eval(), InputCache()
+    base = torch.zeros(64)
+    with torch.no_grad(), input_cache_scope() as scope:
+        cache.get("views", (), owner, lambda: (base[:8], base[8:], {"again": base}))
+        assert scope.used == base.untyped_storage().nbytes()
+        cache.get("other", (), owner, lambda: torch.zeros(16))
+        assert scope.used == base.untyped_storage().nbytes() + 64
+        reset_input_cache(nn.Sequential())           # no module of this model holds them
+        assert scope.used > 0
