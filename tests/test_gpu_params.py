@@ -63,3 +63,23 @@ def test_block_from_checkpoint(device, tmp_path):
                                    inp.seq_mask.to(device))
     assert_parity(got_pair, want_pair, TOL_FP32, "pair (checkpoint weights)")
     assert_parity(got_single, want_single, TOL_FP32, "single (checkpoint weights)")
+
+
+def test_load_waits_for_work_queued_on_the_current_stream(device, tmp_path):
+    """The device arena may be a block whose previous tensor is still to be read by work
+    queued on the current stream; the upload's copies must start after that work."""
+    announce("load_params after queued work")
+    g = torch.Generator().manual_seed(5)
+    state = {"w": torch.randn(1 << 18, generator=g)}           # 1 MiB: the arena's size
+    paths = write_checkpoint(tmp_path, state, parts=1)
+    cpu = load_params(paths)
+    src = torch.randn(1 << 18, generator=g).to(device)         # a 1 MiB block of the same pool
+    want = src.cpu() * 3
+    torch.cuda.synchronize()
+    torch.cuda._sleep(50_000_000)                              # holds the current stream
+    out = src * 3                                              # reads src after the spin
+    del src                                                    # its block is free for reuse
+    gpu = load_params(paths, device=device, staging_bytes=1 << 16)
+    torch.cuda.synchronize()
+    assert torch.equal(out.cpu(), want)
+    assert torch.equal(gpu["block/w"].cpu(), cpu["block/w"])

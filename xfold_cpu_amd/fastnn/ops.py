@@ -261,6 +261,7 @@ class AttentionOperands:
 
 _SHARED_OPERANDS: "collections.OrderedDict" = collections.OrderedDict()
 _SHARED_OPERANDS_MAX = 8
+_SHARED_OPERANDS_LOCK = threading.Lock()
 
 
 def shared_attention_operands(B: int, T: int, H: int, Dh: int, device: torch.device) -> AttentionOperands:
@@ -271,13 +272,13 @@ def shared_attention_operands(B: int, T: int, H: int, Dh: int, device: torch.dev
     released (the caching allocator keeps it from reuse until the queued work is done)."""
     device = torch.device(device)
     key = (B, T, H, Dh, device, nh.stream_of(device), threading.get_ident())
-    ops_ = _SHARED_OPERANDS.get(key)
-    if ops_ is None:
-        ops_ = _SHARED_OPERANDS[key] = AttentionOperands(B, T, H, Dh, device)
+    with _SHARED_OPERANDS_LOCK:                  # one table for every host thread
+        ops_ = _SHARED_OPERANDS.pop(key, None)
+        if ops_ is None:
+            ops_ = AttentionOperands(B, T, H, Dh, device)
+        _SHARED_OPERANDS[key] = ops_             # (re)inserted as the most recent
         while len(_SHARED_OPERANDS) > _SHARED_OPERANDS_MAX:
             _SHARED_OPERANDS.popitem(last=False)
-    else:
-        _SHARED_OPERANDS.move_to_end(key)
     return ops_
 
 

@@ -192,9 +192,12 @@ def load_params(paths, device: Optional[Union[str, torch.device]] = None,
             offset += (head[4] + _ALIGN - 1) // _ALIGN * _ALIGN
             stream.seek(head[4], os.SEEK_CUR)
         arena = torch.empty(max(offset, 1), dtype=torch.uint8, device=device)
+        # The arena comes from the caching allocator on the current stream: its block may
+        # still be read by work queued there, so the copies start after that work.
+        copy_stream = torch.cuda.Stream(device=device)
+        copy_stream.wait_stream(torch.cuda.current_stream(device))
         staging = [torch.empty(staging_bytes, dtype=torch.uint8, pin_memory=True) for _ in range(2)]
         done = [None, None]
-        copy_stream = torch.cuda.Stream(device=device)
         slot, fill = 0, 0
         pending = []                                  # (arena offset, staging offset, bytes) of this slot
 
