@@ -66,6 +66,22 @@ def assert_parity(actual, expected, tol, what=""):
 # result also has): the stored value is quantised to 8 significant bits, and one step of
 # that quantum at the largest elements is ~2e-2 of the RMS by itself.
 FLOOR_FACTOR = 1.5
+# With a floor, the RMS error must also stay within FLOOR_RMS_FACTOR x the floor's own RMS
+# error (plus RMS_SLACK of the output RMS, for floors that are exact to a few 1e-4): the
+# floor's RMS error is a mean over every element, so unlike the max it moves with kernel
+# error well below one bf16 step, and a kernel twice as inaccurate as bf16 arithmetic
+# needs fails it.
+FLOOR_RMS_FACTOR = 1.25
+RMS_SLACK = 1e-3
+# Small outputs: the floor's max error is then the max of a few thousand draws, a poor
+# estimate of the spread of a second realisation of the same roundings. On the 2-block
+# diffusion transformer at 2-16 tokens (20 seeded cases, 1-3 samples, 512-8192 outputs) the
+# HIP max error ranged over 0.59-1.41x the floor's max (the RMS ratio stayed within
+# 0.95-1.09x), and one case reached 1.64x: 5.2x its RMS error, at an element of magnitude
+# 2.2 two and a half bf16 steps from the exact value after four bf16 residual roundings.
+# The max guard therefore also admits MAX_SIGMAS x the floor's RMS error; at the benchmark
+# configurations that term is below FLOOR_FACTOR x the floor's max and changes nothing.
+MAX_SIGMAS = 6.0
 
 
 def bf16_stored(t):
@@ -125,18 +141,25 @@ def stored_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
 
 
 def assert_parity_bf16(actual, expected, what="", floor=None):
-    """bf16-mode parity, relative to RMS(expected): RMS error <= TOL_BF16, and max error
-    <= max(TOL_BF16, FLOOR_FACTOR x the max error of `floor`, the case's bf16 floor); for a
+    """bf16-mode parity, relative to RMS(expected): RMS error <= TOL_BF16 and, with a
+    floor, <= FLOOR_RMS_FACTOR x the floor's RMS error + RMS_SLACK; max error <=
+    max(TOL_BF16, FLOOR_FACTOR x the max error of `floor`, the case's bf16 floor,
+    MAX_SIGMAS x the floor's RMS error). For a
     bf16 `actual` both max errors are net of half an ulp per element (stored_rel_err)."""
     stored = actual.dtype == torch.bfloat16
     max_of = stored_rel_err if stored else rel_err
     rms_err = rms_rel_err(actual, expected)
     max_err = max_of(actual, expected)
     floor_err = max_of(floor, expected) if floor is not None else 0.0
-    guard = max(TOL_BF16, FLOOR_FACTOR * floor_err)
-    print(f"[parity] {what}: rms {rms_err:.3e} max {max_err:.3e} floor {floor_err:.3e} "
-          f"guard {guard:.3e}{' (net of storage rounding)' if stored else ''}", flush=True)
-    assert rms_err <= TOL_BF16, f"{what}: rms|diff|/rms = {rms_err:.3e} > {TOL_BF16:.1e}"
+    floor_rms = rms_rel_err(floor, expected) if floor is not None else None
+    guard = max(TOL_BF16, FLOOR_FACTOR * floor_err, MAX_SIGMAS * (floor_rms or 0.0))
+    rms_guard = TOL_BF16 if floor is None else min(TOL_BF16, FLOOR_RMS_FACTOR * floor_rms + RMS_SLACK)
+    ratio = f" ({rms_err / floor_rms:.2f}x)" if floor_rms else ""
+    print(f"[parity] {what}: rms {rms_err:.3e} floor-rms {floor_rms if floor_rms is not None else 0.0:.3e}{ratio} "
+          f"rms-guard {rms_guard:.3e} | max {max_err:.3e} floor {floor_err:.3e} guard {guard:.3e}"
+          f"{' (net of storage rounding)' if stored else ''}", flush=True)
+    assert rms_err <= rms_guard, (f"{what}: rms|diff|/rms = {rms_err:.3e} > {rms_guard:.3e} "
+                                  f"(floor rms {floor_rms})")
     assert max_err <= guard, (f"{what}: max|diff|/rms = {max_err:.3e} > {guard:.3e} "
                               f"(floor {floor_err:.3e})")
     return rms_err, max_err
