@@ -112,8 +112,10 @@ class Bf16Operands(TorchFunctionMode):
     """While active, every matrix product of the restatement (``nn.Linear``'s
     ``F.linear``, ``torch.matmul``/``@``, ``torch.einsum``, ``bmm``/``mm``) sees its
     operands rounded to bf16 and keeps its accumulation in the caller's dtype (fp32 or
-    float64); the contraction (the restatement's only ``einsum``) and the attention output
-    (a product whose left operand is a softmax) are rounded to bf16 as well; LayerNorm,
+    float64); the contraction (the restatement's only ``einsum``), the attention output
+    (a product whose left operand is a softmax) and the output of a Linear whose weight is
+    marked ``_bf16_linear_output`` (the DiffusionTransformer's pair logits, an autocast
+    Linear output the reference keeps between calls) are rounded to bf16 as well; LayerNorm,
     softmax, sigmoid, the mask fill and the residual adds stay exact, except that an
     in-place add into a tensor marked by :func:`mark_residual` is rounded to bf16
     afterwards. Running ``oracle.restatement``'s modules under this mode
@@ -128,6 +130,8 @@ class Bf16Operands(TorchFunctionMode):
     def __torch_function__(self, func, types, args=(), kwargs=None):
         kwargs = kwargs or {}
         name = getattr(func, "__name__", "")
+        marked = name == "linear" and getattr(args[1] if len(args) > 1 else kwargs.get("weight"),
+                                              "_bf16_linear_output", False)
         if self.float64 and not name.endswith("_"):
             # Every out-of-place op evaluates in float64 (fp32 parameters and inputs are
             # exact in it): the same floor with another accumulation precision, hence
@@ -145,6 +149,7 @@ class Bf16Operands(TorchFunctionMode):
             return func(*args, **kwargs)
         stored = name == "einsum" or getattr(args[0], "_softmax_output", False)
         if name == "linear":
+            stored = stored or marked
             args = tuple(_round_operand(a) if i < 2 else a for i, a in enumerate(args))
             if "weight" in kwargs:
                 kwargs = dict(kwargs, weight=_round_operand(kwargs["weight"]))

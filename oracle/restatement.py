@@ -567,6 +567,11 @@ class DiffusionTransformer(nn.Module):
         self.pair_logits_projection = nn.ModuleList(
             [nn.Linear(c_pair_cond, super_block_size * num_head, bias=False)
              for _ in range(self.num_super_blocks)])
+        # The pair logits are an autocast Linear's output, kept between the sampler's calls
+        # (:255-265): bf16 under bf16 autocast. oracle.bf16_floor rounds the outputs of a
+        # Linear whose weight carries this mark; the exact evaluation ignores it.
+        for projection in self.pair_logits_projection:
+            projection.weight._bf16_linear_output = True
         self.self_attention = nn.ModuleList(
             [SelfAttention(c_act, c_single_cond, use_single_cond=True) for _ in range(num_blocks)])
         self.transition_block = nn.ModuleList(

@@ -298,8 +298,11 @@ def diffusion_transformer_hip(module: nn.Module, act: torch.Tensor, mask: torch.
         projs = [module.pair_logits_projection[s].weight for s in range(module.num_super_blocks)]
         w_all = nh.derived_weight(module, f"pair_logits:{dtype}", projs,
                                   lambda *ws: torch.cat([w.detach() for w in ws], dim=0).to(dtype).contiguous())
+        # bf16 logits, the dtype of the reference's autocast Linear output (half the bytes of
+        # fp32: at N=768 all 24 blocks' logits take 453 MB and fit the input cache's budget).
         packed = _cached(module, "pair_logits_packed", (pair_cond, heads),
-                         lambda: ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln),
+                         lambda: ops.pair_attention_bias(pair_cond, ln.weight, ln.bias, ln.eps, w_all, owner=ln,
+                                                         out_dtype=torch.bfloat16),
                          modules=(ln, module.pair_logits_projection))
         operands = _block_operands(module, act, mask)
         for index in range(n_blocks):
