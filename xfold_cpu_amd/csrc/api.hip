@@ -52,13 +52,15 @@ namespace {
 struct TimedEvent {
   std::string name;
   hipEvent_t start, stop;
+  double work;
 };
 std::mutex g_timing_mutex;
 bool g_timing_enabled = false;
 std::vector<TimedEvent> g_timed;
 }  // namespace
 
-KernelTimer::KernelTimer(const char *name, hipStream_t stream) : name_(name), stream_(stream) {
+KernelTimer::KernelTimer(const char *name, hipStream_t stream, double work)
+    : name_(name), stream_(stream), work_(work) {
   if (!g_timing_enabled) return;
   hipEvent_t e;
   if (hipEventCreate(&e) != hipSuccess) return;
@@ -79,7 +81,7 @@ KernelTimer::~KernelTimer() {
     return;
   }
   std::lock_guard<std::mutex> lock(g_timing_mutex);
-  g_timed.push_back({name_, static_cast<hipEvent_t>(start_), e});
+  g_timed.push_back({name_, static_cast<hipEvent_t>(start_), e, work_});
 }
 
 static bool float_dtype(int d) { return d == XFH_F32 || d == XFH_BF16; }
@@ -182,9 +184,14 @@ void xfh_set_kernel_timing(int enable) {
 }
 
 int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches) {
-  XFH_REQUIRE(name && total_ms && launches, "kernel_timing_read: null argument");
+  double work = 0.0;
+  return xfh_kernel_timing_read_work(name, total_ms, launches, &work);
+}
+
+int xfh_kernel_timing_read_work(const char *name, double *total_ms, int64_t *launches, double *work) {
+  XFH_REQUIRE(name && total_ms && launches && work, "kernel_timing_read: null argument");
   std::lock_guard<std::mutex> lock(g_timing_mutex);
-  double total = 0.0;
+  double total = 0.0, done = 0.0;
   int64_t count = 0;
   std::vector<TimedEvent> keep;
   for (auto &t : g_timed) {
@@ -197,6 +204,7 @@ int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches
     if (hipEventElapsedTime(&ms, t.start, t.stop) != hipSuccess)
       return fail(XFH_EHIP, "kernel_timing_read: elapsed time failed");
     total += ms;
+    done += t.work;
     ++count;
     (void)hipEventDestroy(t.start);
     (void)hipEventDestroy(t.stop);
@@ -204,6 +212,7 @@ int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches
   g_timed.swap(keep);
   *total_ms = total;
   *launches = count;
+  *work = done;
   return XFH_OK;
 }
 

@@ -39,13 +39,16 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 
 // Opt-in per-kernel timing (xfh_set_kernel_timing): when enabled, a KernelTimer brackets a
 // launch with HIP events recorded on the launch stream.
+// `work` (algorithmic FLOPs or bytes of the launch) is summed with the durations, so a
+// kernel launched on several shapes has one aggregate rate.
 class KernelTimer {
  public:
-  KernelTimer(const char *name, hipStream_t stream);
+  KernelTimer(const char *name, hipStream_t stream, double work = 0.0);
   ~KernelTimer();
  private:
   const char *name_;
   hipStream_t stream_;
+  double work_;
   void *start_ = nullptr;
 };
 // Compute units of the current device (cached per device).

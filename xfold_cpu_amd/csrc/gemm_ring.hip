@@ -511,7 +511,7 @@ bool gemm_ring_supported(const GemmArgs &p, int out_dtype) {
 int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  KernelTimer timer("gemm_ring", s);
+  KernelTimer timer("gemm_ring", s, 2.0 * double(p.M) * double(p.N) * double(p.K) * double(batch));
   const RingPick pick = pick_ring(p, batch, glu, cus);
   const int bn = pick == RingPick::XWide ? 192 : pick == RingPick::Shallow ? 128 : pick == RingPick::Mid ? 96 : 64;
   // Per-XCD row runs when row blocks span several tiles, the whole B operand fits comfortably

@@ -45,6 +45,8 @@ SIGNATURES = {
     "xfh_last_error": (ctypes.c_char_p, []),
     "xfh_set_kernel_timing": (None, [_i]),
     "xfh_kernel_timing_read": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _pi64]),
+    "xfh_kernel_timing_read_work": (_i, [ctypes.c_char_p, ctypes.POINTER(ctypes.c_double), _pi64,
+                                         ctypes.POINTER(ctypes.c_double)]),
     "xfh_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _f, _p, _i, _p]),
     "xfh_adaptive_layer_norm": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _i64, _f, _p, _i, _p]),
     "xfh_linear": (_i, [_p, _i64, _p, _p, _i64, _i64, _i64, _i, _p, _i64, _i, _i, _p, _i64, _i64, _p]),
@@ -127,6 +129,14 @@ def kernel_timing_read(name: str):
     total, count = ctypes.c_double(), ctypes.c_int64()
     call("xfh_kernel_timing_read", name.encode(), ctypes.byref(total), ctypes.byref(count))
     return total.value, count.value
+
+
+def kernel_timing_read_work(name: str):
+    """(total milliseconds, launches, total declared FLOPs) recorded for ``name`` since the
+    last read."""
+    total, count, work = ctypes.c_double(), ctypes.c_int64(), ctypes.c_double()
+    call("xfh_kernel_timing_read_work", name.encode(), ctypes.byref(total), ctypes.byref(count), ctypes.byref(work))
+    return total.value, count.value, work.value
 
 
 @functools.lru_cache(maxsize=None)
