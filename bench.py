@@ -1,7 +1,7 @@
 """Benchmark of the HIP Pairformer path on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config C2] [--no-cpu-baseline] [--no-c3]
-                    [--no-cached] [--graph]
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--config C2] [--no-cpu-baseline]
+                    [--no-c3] [--no-c4] [--no-c5] [--no-cached] [--graph]
 
 A step is one forward pass of the configured workload over synthetic inputs already in
 HBM: C2 (default, the metric's N=384 configuration) = one Pairformer pair block at N=384
@@ -11,10 +11,12 @@ at N=1536. ``value`` is milliseconds per Pairformer block (per transformer pass 
 
 One JSON line with the driver's fields plus ``roofline`` (the dominant kernel, timed with
 HIP events on its launch stream inside this run; ``traffic`` from the rocprofv3 counter
-record of the same kernel sources), ``kernels`` (every pair kernel's rate), ``c3`` (the
-48-block N=768 trunk timed in the same run, with its own roofline, when the configuration
-is the default C2) and ``cpu_baseline`` (restatements of the reference's torch and cpp
-backends timed on the host cores: 1 warm-up, median of 3).
+record of the same kernel sources), ``kernels`` (every pair kernel's rate) and
+``cpu_baseline`` (restatements of the reference's torch and cpp backends timed on the host
+cores: 1 warm-up, median of 3). With the default C2 configuration the other GPU
+configurations are timed in the same run, each with its own roofline, kernels and CPU
+legs: ``c3`` (the 48-block N=768 trunk, the north-star target), ``c4`` (the diffusion
+transformer, uncached and inside an input-cache scope) and ``c5`` (the N=1536 block).
 """
 
 from __future__ import annotations
@@ -49,6 +51,10 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-c3", action="store_true",
                    help="with the default C2 configuration, skip the 48-block C3 trunk timed beside it")
+    p.add_argument("--no-c4", action="store_true",
+                   help="with the default C2 configuration, skip the C4 diffusion transformer timed beside it")
+    p.add_argument("--no-c5", action="store_true",
+                   help="with the default C2 configuration, skip the C5 N=1536 block timed beside it")
     p.add_argument("--no-cached", action="store_true",
                    help="with C4, skip the input-cache forward timed beside the uncached one")
     p.add_argument("--graph", action="store_true",
@@ -126,14 +132,13 @@ def build_workload(cfg_name, device):
     return step, 1, workload, cfg
 
 
-def time_cached_diffusion(device, steps, warmup):
+def time_cached_diffusion(step, steps, warmup):
     """ms per C4 forward inside an input-cache scope (the reference's InputCache rules, as
-    its sampler runs 200 forwards per example): the pair logits and the block conditioning
-    are computed in the first forward and reused. Reported beside ``value``, not as it."""
+    its sampler runs 200 forwards per example): the packed pair logits of all 24 blocks are
+    computed in the first forward and reused. Reported beside the uncached time."""
     import torch
     from xfold_cpu_amd.fastnn import config
     from xfold_cpu_amd.nn.cache import input_cache_scope
-    step, _, _, _ = build_workload("C4", device)
     saved = config.input_cache_enabled
     config.input_cache_enabled = True
     try:
@@ -152,31 +157,32 @@ def time_cached_diffusion(device, steps, warmup):
     return start.elapsed_time(stop) / steps
 
 
-COUNTER_FILES = {384: ROOT / "profiles" / "counters_c2_n384.md", 768: ROOT / "profiles" / "counters_c3_n768.md"}
+COUNTER_FILES = {"C2": ROOT / "profiles" / "counters_c2_n384.md", "C3": ROOT / "profiles" / "counters_c3_n768.md",
+                 "C4": ROOT / "profiles" / "counters_c4_n768.md", "C5": ROOT / "profiles" / "counters_c5_n1536.md"}
 
 
-def attention_traffic(n):
-    """HBM bytes per grid_attention_kernel launch at N tokens, from the rocprofv3 FETCH_SIZE /
-    WRITE_SIZE passes recorded in profiles/counters_*.md (calibrated against a 512 MiB
-    read+write kernel in the same run). Counters cannot be read inside this process, so the
-    figure is the recorded measurement; it is returned only while the attention kernel's
+def recorded_traffic(cfg_name, kernel):
+    """HBM bytes per launch of ``kernel`` in configuration ``cfg_name``, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes recorded in profiles/counters_*.md (calibrated against a
+    512 MiB read+write kernel in the same run). Counters cannot be read inside this process,
+    so the figure is the recorded measurement; it is returned only while the kernel's
     sources hash to the digest recorded with it, else (None, reason)."""
     import hashlib
-    path = COUNTER_FILES.get(n)
+    path = COUNTER_FILES.get(cfg_name)
     if path is None or not path.exists():
-        return None, f"no counter record for N={n}"
+        return None, f"no counter record for {cfg_name}"
     rec = None
     for line in path.read_text().splitlines():
-        if line.startswith('{"counters": "grid_attention_kernel"'):
+        if line.startswith(f'{{"counters": "{kernel}"'):
             rec = json.loads(line)
     if rec is None:
-        return None, f"{path.name} holds no machine-readable record"
+        return None, f"{path.name} holds no machine-readable record for {kernel}"
     h = hashlib.sha256()
     for src in rec["sources"]:
         h.update((ROOT / src).read_bytes())
     if h.hexdigest() != rec["sources_sha256"]:
-        return None, (f"stale: {path.name} was measured at commit {rec['commit']} on other attention "
-                      "kernel sources")
+        return None, (f"stale: {path.name} was measured at commit {rec['commit']} on other {kernel} "
+                      "sources")
     return rec["traffic_bytes"], f"{path.name} (commit {rec['commit']}, sources match)"
 
 
@@ -184,7 +190,7 @@ PAIR_TIMERS = ("transition", "trimul_project", "trimul_contract", "trimul_output
                "grid_attention", "grid_output", "pair_bias")
 
 
-def kernel_roofline(step, n, steps):
+def kernel_roofline(step, cfg_name, n, steps):
     """Average launch duration of every pair-stack kernel inside the block workload, from HIP
     events the library records around each launch on the launch stream, with its HBM or MFMA
     rate (algorithmic bytes / FLOPs of one launch, xfold_cpu_amd.kernel_bench). Returns the
@@ -227,12 +233,62 @@ def kernel_roofline(step, n, steps):
     heads, d = 4, 32
     flops = 4.0 * n * heads * n * n * d            # Q.K^T and P.V over all N^3 logits
     achieved = flops / (ms * 1e-3) / 1e12
-    traffic, traffic_src = attention_traffic(n)
+    traffic, traffic_src = recorded_traffic(cfg_name, "grid_attention_kernel")
     return {"kernel": "grid_attention_kernel (triangle attention core)", "bound": "mfma",
             "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
             "avg_launch_ms": round(ms, 4), "launches": launches, "flops_per_launch": flops,
             "shape": f"B={n} H={heads} Q=K={n} D={d} bf16"}, kernels
+
+
+DIFFUSION_TIMERS = ("gemm_ring", "mha_attention", "pair_bias", "layer_norm")
+
+
+def diffusion_roofline(step, cfg_name, steps):
+    """The diffusion transformer's kernels inside its forward: average launch time and the
+    rate of the algorithmic FLOPs each launch declares (every Linear's 2 M N K for gemm_ring,
+    4 B H N^2 Dv for the attention), from HIP events on the launch stream. The roofline
+    object is the dominant kernel, gemm_ring (all Linears of the forward aggregated: their
+    FLOPs over their summed launch time)."""
+    import torch
+    from xfold_cpu_amd.fastnn import native_hip
+
+    native_hip.set_kernel_timing(True)
+    try:
+        step()                                        # dropped: a process's first event records read high
+        torch.cuda.synchronize()
+        for name in DIFFUSION_TIMERS:
+            native_hip.kernel_timing_read_work(name)
+        torch.cuda._sleep(20_000_000)
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        native_hip.set_kernel_timing(False)
+    kernels = {}
+    for name in DIFFUSION_TIMERS:
+        total_ms, launches, work = native_hip.kernel_timing_read_work(name)
+        if not launches:
+            continue
+        rec = dict(avg_us=round(total_ms / launches * 1e3, 2), launches=launches,
+                   ms_per_forward=round(total_ms / steps, 4))
+        if work:
+            tflops = work / (total_ms * 1e-3) / 1e12
+            rec.update(tflops=round(tflops, 1), mfma_frac=round(tflops / PEAK_BF16_TFLOPS, 4))
+        kernels[name + "_kernel"] = rec
+    g = kernels.get("gemm_ring_kernel")
+    if g is None:
+        return None, kernels
+    ms_all = g["ms_per_forward"] * steps
+    flops = g["tflops"] * 1e12 * ms_all * 1e-3
+    traffic, traffic_src = recorded_traffic(cfg_name, "gemm_ring_kernel")
+    return {"kernel": "gemm_ring_kernel (every Linear of the forward, aggregated over its shapes)",
+            "bound": "mfma", "achieved": g["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(g["tflops"] / PEAK_BF16_TFLOPS, 4), "traffic": traffic, "traffic_source": traffic_src,
+            "avg_launch_ms": round(g["avg_us"] / 1e3, 4), "launches": g["launches"],
+            "flops_per_launch": round(flops / g["launches"]),
+            "shape": "per block: [5*768, 768] x 768->3072 (q, k, v, gate), 768->768 (AdaLNZero), "
+                     "768->3072 (GLU), 1536->768; plus the batched conditioning Linears"}, kernels
 
 
 def host_cpu():
@@ -318,6 +374,67 @@ def cpu_workload(cfg_name, leg):
     return fn, what, 1, blocks
 
 
+C5_SAMPLE_ROWS = (32, 96)
+
+
+def cpu_c5_sample(leg):
+    """C5 (one pair block at N=1536) on the host, bounded: both triangle multiplications and
+    the transition in full; each triangle-attention node on 32 and on 96 of its 1536 batch
+    rows, extrapolated linearly to all rows (every batch row costs the same: its own N x N
+    logits per head over the shared bias; the intercept is the full LayerNorm and bias
+    projection). One timed run of each part after a warm-up pair block at N=64. Returns
+    (ms per block, parts, description)."""
+    import torch
+    from oracle import restatement as R
+    from xfold_cpu_amd.synthetic import CONFIGS, init_module_, pair_block_inputs
+
+    cfg = CONFIGS["C5"]
+    n = cfg["n"]
+    block = init_module_(R.PairformerBlock(with_single=False).eval(), seed=0)
+    if leg == "cpp":
+        from oracle import cpp_port
+        cpp_port.load()
+        tri = cpp_port.triangle_multiplication_cpp
+        rows_fn = cpp_port.grid_self_attention_rows_cpp
+        trans = cpp_port.transition_cpp
+        warm = cpp_port.PairformerBlockCpp(block)
+    else:
+        tri = lambda m, p, mask: m(p, mask)  # noqa: E731
+        rows_fn = R.grid_self_attention_rows
+        trans = lambda m, p: m(p)  # noqa: E731
+        warm = block
+    autocast = lambda: torch.amp.autocast("cpu", dtype=torch.bfloat16)  # noqa: E731
+    small = pair_block_inputs(64, pad=4, seed=0, with_single=False)
+    chunked = lambda *a, **k: R.dot_product_attention_chunked(*a, rows_per_chunk=32, **k)  # noqa: E731
+    with torch.inference_mode(), autocast():
+        warm(small.pair.bfloat16(), small.pair_mask, attention=chunked)
+    inp = pair_block_inputs(n, pad=cfg["pad"], random_pad=cfg["random_pad"], seed=0, with_single=False)
+    pair, mask = inp.pair.bfloat16(), inp.pair_mask
+
+    def timed(fn):
+        t0 = time.perf_counter()
+        with torch.inference_mode(), autocast():
+            fn()
+        return (time.perf_counter() - t0) * 1e3
+    parts = {}
+    parts["triangle_multiplication_outgoing"] = timed(lambda: tri(block.triangle_multiplication_outgoing, pair, mask))
+    parts["triangle_multiplication_incoming"] = timed(lambda: tri(block.triangle_multiplication_incoming, pair, mask))
+    for node in ("pair_attention1", "pair_attention2"):
+        module = getattr(block, node)
+        (r0, r1) = C5_SAMPLE_ROWS
+        t0 = timed(lambda: rows_fn(module, pair, mask, torch.arange(r0)))
+        t1 = timed(lambda: rows_fn(module, pair, mask, torch.arange(r0, r0 + r1)))
+        per_row = max(t1 - t0, 0.0) / (r1 - r0)
+        parts[node] = t0 + per_row * (n - r0)
+        parts[node + "_sample_ms"] = [round(t0, 1), round(t1, 1)]
+    parts["pair_transition"] = timed(lambda: trans(block.pair_transition, pair))
+    total = sum(v for k, v in parts.items() if not k.endswith("_sample_ms"))
+    what = (f"one pair block at N={n}, bf16 CPU autocast: triangle multiplications and transition in full, "
+            f"each attention node timed on {C5_SAMPLE_ROWS[0]} and {C5_SAMPLE_ROWS[1]} batch rows and "
+            f"extrapolated linearly to {n}; one run per part after an N=64 warm-up block")
+    return total, {k: (round(v, 1) if isinstance(v, float) else v) for k, v in parts.items()}, what
+
+
 def cpu_baseline(cfg_name, runs=3):
     """The reference's CPU backends restated and timed on this host (BASELINE.md protocol):
     1 warm-up then the median of ``runs`` runs, on ``cpu_threads()`` threads. The torch leg is
@@ -329,6 +446,15 @@ def cpu_baseline(cfg_name, runs=3):
     torch.set_num_threads(threads)
     legs = {}
     for leg in ("torch", "cpp"):
+        if cfg_name == "C5":
+            try:
+                total, parts, what = cpu_c5_sample(leg)
+            except (ImportError, RuntimeError, OSError) as err:
+                legs[leg] = {"status": f"unavailable: {err}"}
+                continue
+            legs[leg] = {"ms_per_block": round(total, 1), "parts_ms": parts, "sample": what}
+            log(f"cpu {leg}: {legs[leg]}")
+            continue
         try:
             fn, what, per_call, factor = cpu_workload(cfg_name, leg)
         except (ImportError, RuntimeError, OSError) as err:
@@ -346,8 +472,9 @@ def cpu_baseline(cfg_name, runs=3):
     value = torch_leg.get("ms_per_block", torch_leg.get("ms_per_forward"))
     return {"value": value, "unit": "ms per Pairformer block" if cfg_name != "C4" else "ms per transformer forward",
             "cores": threads, "kind": "port",
-            "sample": f"{torch_leg.get('sample', cfg_name)}; 1 warm-up + median of {runs}; "
-                      "restatements of the reference's torch and cpp (af3_kernels) backends",
+            "sample": (f"{torch_leg.get('sample', cfg_name)}" +
+                       ("" if cfg_name == "C5" else f"; 1 warm-up + median of {runs}") +
+                       "; restatements of the reference's torch and cpp (af3_kernels) backends"),
             "legs": legs, "host": host_cpu()}
 
 
@@ -385,9 +512,13 @@ def run_config(cfg_name, steps, warmup, device, graph=False):
     log(f"{cfg_name} timed {steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
     roof, kernels = None, None
     if cfg["kind"] != "diffusion":
-        roof, kernels = kernel_roofline(step, cfg["n"], max(1, min(steps, 10)))
+        roof, kernels = kernel_roofline(step, cfg_name, cfg["n"], max(1, min(steps, 10)))
         log(f"{cfg_name} roofline: {roof}")
-    return dict(ms_step=ms_step, blocks=blocks, workload=workload, cfg=cfg, roofline=roof, kernels=kernels)
+    else:
+        roof, kernels = diffusion_roofline(step, cfg_name, max(1, min(steps, 10)))
+        log(f"{cfg_name} roofline: {roof}")
+    return dict(ms_step=ms_step, blocks=blocks, workload=workload, cfg=cfg, roofline=roof, kernels=kernels,
+                step=step)
 
 
 def main():
@@ -408,27 +539,42 @@ def main():
     ms_step, blocks, cfg = res["ms_step"], res["blocks"], res["cfg"]
     value = ms_step / blocks
 
-    # The north-star target (C3, the 48-block trunk at N=768) is timed beside the metric's
-    # N=384 configuration in the default run.
+    # With the default C2 configuration (the metric's N=384 block) the other GPU
+    # configurations are timed in the same run: C3 (the north-star 48-block trunk at N=768),
+    # C4 (the diffusion transformer) and C5 (the N=1536 block).
     extra = {}
     if args.config == "C4" and not args.no_cached:
-        extra["cached_forward_ms"] = round(time_cached_diffusion(device, args.steps, max(1, args.warmup)), 4)
+        extra["cached_forward_ms"] = round(time_cached_diffusion(res["step"], args.steps, max(1, args.warmup)), 4)
         log(f"C4 with the input cache: {extra['cached_forward_ms']} ms per forward")
-    c3 = None
-    if args.config == "C2" and not args.no_c3:
-        c3_steps, c3_warmup = DEFAULT_STEPS["C3"]
-        r3 = run_config("C3", c3_steps, c3_warmup, device, graph=args.graph)
-        c3 = {"ms_per_block": round(r3["ms_step"] / r3["blocks"], 4), "ms_per_trunk": round(r3["ms_step"], 3),
-              "steps": c3_steps, "warmup": c3_warmup, "config": r3["workload"], "roofline": r3["roofline"],
-              "kernels": r3["kernels"]}
+    subs = {}
+    if args.config == "C2":
+        for name, skip in (("C3", args.no_c3), ("C4", args.no_c4), ("C5", args.no_c5)):
+            if skip:
+                continue
+            steps, warmup = DEFAULT_STEPS[name]
+            r = run_config(name, steps, warmup, device, graph=args.graph)
+            if name == "C4":
+                sub = {"ms_per_forward": round(r["ms_step"], 4)}
+                if not args.no_cached:
+                    sub["cached_forward_ms"] = round(time_cached_diffusion(r["step"], steps, warmup), 4)
+                    log(f"C4 with the input cache: {sub['cached_forward_ms']} ms per forward")
+            else:
+                sub = {"ms_per_block": round(r["ms_step"] / r["blocks"], 4)}
+                if name == "C3":
+                    sub["ms_per_trunk"] = round(r["ms_step"], 3)
+            sub.update(steps=steps, warmup=warmup, config=r["workload"], roofline=r["roofline"],
+                       kernels=r["kernels"])
+            subs[name.lower()] = sub
+            del r
+            torch.cuda.empty_cache()
 
     base = None
     if not args.no_cpu_baseline:
         log("cpu baseline (restatements on host cores)")
         base = cpu_baseline(args.config)
-        if c3 is not None:
-            c3["cpu_baseline"] = cpu_baseline("C3")
         log(f"cpu baseline: {base}")
+        for key, sub in subs.items():
+            sub["cpu_baseline"] = cpu_baseline(key.upper())
 
     if args.copy_calibration_mb:
         # One elementwise kernel (bitwise_not, a name no other kernel of the run has) that
@@ -446,7 +592,7 @@ def main():
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": dtype,
         "data": "synthetic (seeded N(0,1) activations, N(0,1/fan_in) weights)",
         "config": dict(res["workload"], launch="hip graph replay" if args.graph else "eager"),
-        "roofline": res["roofline"], "cpu_baseline": base, "kernels": res["kernels"], "c3": c3, **extra,
+        "roofline": res["roofline"], "cpu_baseline": base, "kernels": res["kernels"], **subs, **extra,
     }
     print(json.dumps(line), flush=True)
 

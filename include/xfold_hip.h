@@ -64,8 +64,9 @@ const char *xfh_last_error(void);
  * releases the recorded intervals of one kernel name. */
 void xfh_set_kernel_timing(int enable);
 int xfh_kernel_timing_read(const char *name, double *total_ms, int64_t *launches);
-/* The same, also summing the algorithmic work (FLOPs) the launches declared: nonzero for
- * "gemm_ring" (2 M N K per GEMM of the launch), 0 for kernels that declare none. */
+/* The same, also summing the algorithmic work (FLOPs) the launches declared: 2 M N K per
+ * GEMM for "gemm_ring", 4 B H Nq N Dv for "grid_attention" and "mha_attention", 0 for
+ * kernels that declare none. */
 int xfh_kernel_timing_read_work(const char *name, double *total_ms, int64_t *launches, double *work);
 
 /* LayerNorm over the last dim of a contiguous [rows, cols] tensor; fp32 statistics.

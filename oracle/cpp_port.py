@@ -135,6 +135,22 @@ def grid_self_attention_cpp(m, pair, mask):
     return out.permute(1, 0, 2) if m.transpose else out
 
 
+def grid_self_attention_rows_cpp(m, pair, mask, rows):
+    """Batch rows ``rows`` of grid_self_attention_cpp (as oracle.restatement's
+    grid_self_attention_rows: the bias from the whole normalised pair, q/k/v/gate from the
+    selected rows), for a CPU sample at sizes where every row would take minutes."""
+    normed = m.act_norm(pair)
+    bias = m.pair_bias_projection(normed).permute(2, 0, 1)
+    if m.transpose:
+        normed = normed.permute(1, 0, 2)
+    x = normed[rows]
+    q, k, v = (R._heads_first(linear_cpp(x, getattr(m, n)), m.num_head)
+               for n in ("q_projection", "k_projection", "v_projection"))
+    out = R._heads_last(dot_product_attention_cpp(q, k, v, mask=mask[rows], bias=bias))
+    out = out * torch.sigmoid(linear_cpp(x, m.gating_query))
+    return linear_cpp(out, m.output_projection)
+
+
 def transition_cpp(m, x):
     """Transition (xfold/nn/primitives.py:33-37): GLU cpp, transition2 a torch Linear."""
     return m.transition2(gated_linear_unit_cpp(m.input_layer_norm(x), m.transition1.weight.T))

@@ -522,7 +522,8 @@ template <class S, typename BT = float> int launch(const GridAttentionArgs &a, c
   const int64_t total = qblocks * rgroups * a.H;
   const int64_t grid = ceil_div(total, 8) * 8;
   if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, std::string(name) + ": problem too large");
-  KernelTimer timer(name, s);
+  // Algorithmic work: Q.K^T and P.V over every (row, head, query, key) at the value head dim.
+  KernelTimer timer(name, s, 4.0 * double(a.B) * a.H * a.Nq * a.N * a.Dv);
   grid_attention_kernel<S, BT><<<dim3(grid), S::T, 0, s>>>(a);
   return check_launch(name);
 }
