@@ -59,9 +59,11 @@ bool g_timing_enabled = false;
 std::vector<TimedEvent> g_timed;
 }  // namespace
 
-KernelTimer::KernelTimer(const char *name, hipStream_t stream, double work)
+KernelTimer::KernelTimer(const char *name, hipStream_t stream, double work, bool dispatch)
     : name_(name), stream_(stream), work_(work) {
   if (!g_timing_enabled) return;
+  enabled_ = true;
+  if (dispatch) return;
   hipEvent_t e;
   if (hipEventCreate(&e) != hipSuccess) return;
   if (hipEventRecord(e, stream_) != hipSuccess) {   // untimed launch: no record is kept
@@ -71,14 +73,29 @@ KernelTimer::KernelTimer(const char *name, hipStream_t stream, double work)
   start_ = e;
 }
 
+bool KernelTimer::dispatch_events() {
+  hipEvent_t a, b;
+  if (hipEventCreate(&a) != hipSuccess) return false;
+  if (hipEventCreate(&b) != hipSuccess) {
+    (void)hipEventDestroy(a);
+    return false;
+  }
+  if (start_) (void)hipEventDestroy(static_cast<hipEvent_t>(start_));   // no bracket start
+  start_ = a;
+  stop_ = b;
+  return true;
+}
+
 KernelTimer::~KernelTimer() {
   if (!start_) return;
-  hipEvent_t e;
-  const bool created = hipEventCreate(&e) == hipSuccess;
-  if (!created || hipEventRecord(e, stream_) != hipSuccess) {
-    if (created) (void)hipEventDestroy(e);
-    (void)hipEventDestroy(static_cast<hipEvent_t>(start_));
-    return;
+  hipEvent_t e = static_cast<hipEvent_t>(stop_);
+  if (!e) {                                                  // bracket: record the end now
+    const bool created = hipEventCreate(&e) == hipSuccess;
+    if (!created || hipEventRecord(e, stream_) != hipSuccess) {
+      if (created) (void)hipEventDestroy(e);
+      (void)hipEventDestroy(static_cast<hipEvent_t>(start_));
+      return;
+    }
   }
   std::lock_guard<std::mutex> lock(g_timing_mutex);
   g_timed.push_back({name_, static_cast<hipEvent_t>(start_), e, work_});

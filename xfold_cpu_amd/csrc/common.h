@@ -1,6 +1,7 @@
 // Shared device/host helpers for the xfold HIP library (gfx950 / CDNA4 only).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,16 +41,32 @@ inline hipStream_t as_stream(void *s) { return reinterpret_cast<hipStream_t>(s);
 // Opt-in per-kernel timing (xfh_set_kernel_timing): when enabled, a KernelTimer brackets a
 // launch with HIP events recorded on the launch stream.
 // `work` (algorithmic FLOPs or bytes of the launch) is summed with the durations, so a
-// kernel launched on several shapes has one aggregate rate.
+// kernel launched on several shapes has one aggregate rate. A launch made through
+// `launch()` is timed by its own dispatch (hipExtLaunchKernelGGL updates the two events
+// with the kernel's start and end), so the interval excludes the event packets around it;
+// otherwise the timer brackets whatever was enqueued in its scope with recorded events.
 class KernelTimer {
  public:
-  KernelTimer(const char *name, hipStream_t stream, double work = 0.0);
+  // dispatch = true: the scope holds one launch made through launch() (nothing is recorded
+  // before it).
+  KernelTimer(const char *name, hipStream_t stream, double work = 0.0, bool dispatch = false);
   ~KernelTimer();
+  template <class K, class... Args>
+  void launch(K kernel, dim3 grid, dim3 block, uint32_t shared, Args... args) {
+    if (enabled_ && dispatch_events()) {
+      hipExtLaunchKernelGGL(kernel, grid, block, shared, stream_, static_cast<hipEvent_t>(start_),
+                            static_cast<hipEvent_t>(stop_), 0, args...);
+      return;
+    }
+    kernel<<<grid, block, shared, stream_>>>(args...);
+  }
  private:
+  bool dispatch_events();                 // the dispatch's own start/stop pair
   const char *name_;
   hipStream_t stream_;
   double work_;
-  void *start_ = nullptr;
+  bool enabled_ = false;
+  void *start_ = nullptr, *stop_ = nullptr;
 };
 // Compute units of the current device (cached per device).
 int device_cu_count(int *cus);

@@ -186,8 +186,8 @@ __global__ __launch_bounds__(64 * T::W, T::WGS) void contraction_kernel(Contract
 template <class T> int launch(const ContractionArgs &a, hipStream_t s) {
   const int64_t total = ceil_div(a.n, T::TBI) * ceil_div(a.n, T::TBJ) * a.channels;
   const int64_t grid = ceil_div(total, 8) * 8;
-  KernelTimer timer("trimul_contract", s);
-  contraction_kernel<T><<<dim3(grid), 64 * T::W, 0, s>>>(a);
+  KernelTimer timer("trimul_contract", s, 2.0 * double(a.channels) * a.n * a.n * a.n, true);
+  timer.launch(contraction_kernel<T>, dim3(grid), dim3(64 * T::W), 0, a);
   return check_launch("contraction");
 }
 

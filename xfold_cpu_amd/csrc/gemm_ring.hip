@@ -438,7 +438,8 @@ using RingShallow = Ring<128, 32, 4, 2>;  // k % 64 != 0
 using RingShallowNarrow = Ring<64, 32, 4, 2>;
 using RingXWide = Ring<192, 64, 2, 2>;     // 1.5x-width tiles: one round where 96 needs two
 
-template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
+template <class G>
+int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s, KernelTimer &timer) {
   const int64_t tiles = ceil_div(p.N, G::BN) * ceil_div(p.M, G::BM);
   if (tiles > (int64_t(1) << 30)) return fail(XFH_EUNSUPPORTED, "gemm_ring: too many tiles");
   dim3 grid(unsigned(ceil_div(p.N, G::BN)), unsigned(ceil_div(p.M, G::BM)), unsigned(batch));
@@ -450,25 +451,25 @@ template <class G> int launch_ring(const GemmArgs &p, int64_t batch, int out_dty
   if (glu) {
     if constexpr (G::NT % 2 == 0) {
       if (p.xcd_split) {
-        if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G, true><<<grid, 256, 0, s>>>(p);
-        else gemm_ring_kernel<float, true, G, true><<<grid, 256, 0, s>>>(p);
+        if (out_dtype == XFH_BF16) timer.launch(gemm_ring_kernel<bf16, true, G, true>, dim3(grid), dim3(256), 0, p);
+        else timer.launch(gemm_ring_kernel<float, true, G, true>, dim3(grid), dim3(256), 0, p);
       } else {
-        if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, true, G><<<grid, 256, 0, s>>>(p);
-        else gemm_ring_kernel<float, true, G><<<grid, 256, 0, s>>>(p);
+        if (out_dtype == XFH_BF16) timer.launch(gemm_ring_kernel<bf16, true, G>, dim3(grid), dim3(256), 0, p);
+        else timer.launch(gemm_ring_kernel<float, true, G>, dim3(grid), dim3(256), 0, p);
       }
     } else {
       return fail(XFH_EUNSUPPORTED, "gemm_ring: GLU needs whole 32-column groups per wavefront");
     }
   } else if (p.attn.q) {
     if (out_dtype != XFH_BF16) return fail(XFH_EUNSUPPORTED, "gemm_ring: the attention layouts are bf16");
-    if (p.xcd_split) gemm_ring_kernel<bf16, false, G, true, true><<<grid, 256, 0, s>>>(p);
-    else gemm_ring_kernel<bf16, false, G, false, true><<<grid, 256, 0, s>>>(p);
+    if (p.xcd_split) timer.launch(gemm_ring_kernel<bf16, false, G, true, true>, dim3(grid), dim3(256), 0, p);
+    else timer.launch(gemm_ring_kernel<bf16, false, G, false, true>, dim3(grid), dim3(256), 0, p);
   } else if (p.xcd_split) {
-    if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, false, G, true><<<grid, 256, 0, s>>>(p);
-    else gemm_ring_kernel<float, false, G, true><<<grid, 256, 0, s>>>(p);
+    if (out_dtype == XFH_BF16) timer.launch(gemm_ring_kernel<bf16, false, G, true>, dim3(grid), dim3(256), 0, p);
+    else timer.launch(gemm_ring_kernel<float, false, G, true>, dim3(grid), dim3(256), 0, p);
   } else {
-    if (out_dtype == XFH_BF16) gemm_ring_kernel<bf16, false, G><<<grid, 256, 0, s>>>(p);
-    else gemm_ring_kernel<float, false, G><<<grid, 256, 0, s>>>(p);
+    if (out_dtype == XFH_BF16) timer.launch(gemm_ring_kernel<bf16, false, G>, dim3(grid), dim3(256), 0, p);
+    else timer.launch(gemm_ring_kernel<float, false, G>, dim3(grid), dim3(256), 0, p);
   }
   return check_launch("gemm_ring");
 }
@@ -511,7 +512,7 @@ bool gemm_ring_supported(const GemmArgs &p, int out_dtype) {
 int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s) {
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
-  KernelTimer timer("gemm_ring", s, 2.0 * double(p.M) * double(p.N) * double(p.K) * double(batch));
+  KernelTimer timer("gemm_ring", s, 2.0 * double(p.M) * double(p.N) * double(p.K) * double(batch), true);
   const RingPick pick = pick_ring(p, batch, glu, cus);
   const int bn = pick == RingPick::XWide ? 192 : pick == RingPick::Shallow ? 128 : pick == RingPick::Mid ? 96 : 64;
   // Per-XCD row runs when row blocks span several tiles, the whole B operand fits comfortably
@@ -528,11 +529,11 @@ int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStre
                                           {"gemm_ring.xwide", "gemm_ring.xwide+xcd"}};
   KernelTimer config_timer(names[int(pick)][q.xcd_split ? 1 : 0], s);
   switch (pick) {
-    case RingPick::Mid: return launch_ring<RingMid>(q, batch, out_dtype, glu, s);
-    case RingPick::XWide: return launch_ring<RingXWide>(q, batch, out_dtype, glu, s);
-    case RingPick::Narrow: return launch_ring<RingNarrow>(q, batch, out_dtype, glu, s);
-    case RingPick::Shallow: return launch_ring<RingShallow>(q, batch, out_dtype, glu, s);
-    default: return launch_ring<RingShallowNarrow>(q, batch, out_dtype, glu, s);
+    case RingPick::Mid: return launch_ring<RingMid>(q, batch, out_dtype, glu, s, timer);
+    case RingPick::XWide: return launch_ring<RingXWide>(q, batch, out_dtype, glu, s, timer);
+    case RingPick::Narrow: return launch_ring<RingNarrow>(q, batch, out_dtype, glu, s, timer);
+    case RingPick::Shallow: return launch_ring<RingShallow>(q, batch, out_dtype, glu, s, timer);
+    default: return launch_ring<RingShallowNarrow>(q, batch, out_dtype, glu, s, timer);
   }
 }
 

@@ -523,8 +523,8 @@ template <class S, typename BT = float> int launch(const GridAttentionArgs &a, c
   const int64_t grid = ceil_div(total, 8) * 8;
   if (grid > (int64_t(1) << 31) - 1) return fail(XFH_EUNSUPPORTED, std::string(name) + ": problem too large");
   // Algorithmic work: Q.K^T and P.V over every (row, head, query, key) at the value head dim.
-  KernelTimer timer(name, s, 4.0 * double(a.B) * a.H * a.Nq * a.N * a.Dv);
-  grid_attention_kernel<S, BT><<<dim3(grid), S::T, 0, s>>>(a);
+  KernelTimer timer(name, s, 4.0 * double(a.B) * a.H * a.Nq * a.N * a.Dv, true);
+  timer.launch(grid_attention_kernel<S, BT>, dim3(grid), dim3(S::T), 0, a);
   return check_launch(name);
 }
 

@@ -322,11 +322,11 @@ int grid_project(const GridProjectArgs &a, int pair_dtype, hipStream_t s) {
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
-  KernelTimer timer("grid_project", s);
+  KernelTimer timer("grid_project", s, 0.0, true);
   if (pair_dtype == XFH_BF16)
-    grid_project_kernel<bf16><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_project_kernel<bf16>, dim3(grid), dim3(512), 0, a);
   else
-    grid_project_kernel<float><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_project_kernel<float>, dim3(grid), dim3(512), 0, a);
   return check_launch("grid_project");
 }
 
@@ -335,15 +335,15 @@ int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStrea
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(steps, 8, cus)));
-  KernelTimer timer("grid_output", s);
+  KernelTimer timer("grid_output", s, 0.0, true);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    grid_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_output_kernel<bf16, bf16>, dim3(grid), dim3(512), 0, a);
   else if (pair_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    grid_output_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_output_kernel<bf16, float>, dim3(grid), dim3(512), 0, a);
   else if (pair_dtype == XFH_F32 && out_dtype == XFH_F32)
-    grid_output_kernel<float, float><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_output_kernel<float, float>, dim3(grid), dim3(512), 0, a);
   else
-    grid_output_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
+    timer.launch(grid_output_kernel<float, bf16>, dim3(grid), dim3(512), 0, a);
   return check_launch("grid_output");
 }
 

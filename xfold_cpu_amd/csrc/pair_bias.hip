@@ -117,13 +117,13 @@ int pair_bias(const PairBiasArgs &a, int pair_dtype, hipStream_t s) {
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
-  KernelTimer timer("pair_bias", s);
+  KernelTimer timer("pair_bias", s, 0.0, true);
   if (pair_dtype == XFH_BF16) {
-    if (a.packed_bf16) pair_bias_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
-    else pair_bias_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
+    if (a.packed_bf16) timer.launch(pair_bias_kernel<bf16, bf16>, dim3(grid), dim3(512), 0, a);
+    else timer.launch(pair_bias_kernel<bf16, float>, dim3(grid), dim3(512), 0, a);
   } else {
-    if (a.packed_bf16) pair_bias_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
-    else pair_bias_kernel<float, float><<<grid, 512, 0, s>>>(a);
+    if (a.packed_bf16) timer.launch(pair_bias_kernel<float, bf16>, dim3(grid), dim3(512), 0, a);
+    else timer.launch(pair_bias_kernel<float, float>, dim3(grid), dim3(512), 0, a);
   }
   return check_launch("pair_bias");
 }

@@ -302,18 +302,18 @@ int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStr
   XFH_TRY(device_cu_count(&cus));
   const int64_t sets = ceil_div(a.rows, int64_t(16));
   const int grid = int(std::min<int64_t>(int64_t(cus) * WG_PER_CU, sets));
-  KernelTimer timer("transition", s);
+  KernelTimer timer("transition", s, 0.0, true);
   const bool in_place = a.accumulate && a.out == a.x;
   if (x_dtype == XFH_BF16 && out_dtype == XFH_BF16 && in_place)
-    transition_kernel<bf16, bf16, true><<<dim3(grid), WAVES * 64, 0, s>>>(a, sets);
+    timer.launch(transition_kernel<bf16, bf16, true>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
   else if (x_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    transition_kernel<bf16, bf16, false><<<dim3(grid), WAVES * 64, 0, s>>>(a, sets);
+    timer.launch(transition_kernel<bf16, bf16, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
   else if (x_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    transition_kernel<bf16, float, false><<<dim3(grid), WAVES * 64, 0, s>>>(a, sets);
+    timer.launch(transition_kernel<bf16, float, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
   else if (x_dtype == XFH_F32 && out_dtype == XFH_F32)
-    transition_kernel<float, float, false><<<dim3(grid), WAVES * 64, 0, s>>>(a, sets);
+    timer.launch(transition_kernel<float, float, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
   else
-    transition_kernel<float, bf16, false><<<dim3(grid), WAVES * 64, 0, s>>>(a, sets);
+    timer.launch(transition_kernel<float, bf16, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
   return check_launch("transition");
 }
 

@@ -303,13 +303,13 @@ int trimul_project(const TriProjectArgs &a, int pair_dtype, hipStream_t s) {
   const bool wide = units32 >= int64_t(cus) * 8 * 4;
   const int64_t units = wide ? units32 : 2 * units32;
   const dim3 grid(unsigned(balanced_grid(units, 8, cus)));
-  KernelTimer timer("trimul_project", s);
+  KernelTimer timer("trimul_project", s, 0.0, true);
   if (pair_dtype == XFH_BF16) {
-    if (wide) trimul_project_kernel<bf16, 2><<<grid, 512, 0, s>>>(a);
-    else trimul_project_kernel<bf16, 1><<<grid, 512, 0, s>>>(a);
+    if (wide) timer.launch(trimul_project_kernel<bf16, 2>, dim3(grid), dim3(512), 0, a);
+    else timer.launch(trimul_project_kernel<bf16, 1>, dim3(grid), dim3(512), 0, a);
   } else {
-    if (wide) trimul_project_kernel<float, 2><<<grid, 512, 0, s>>>(a);
-    else trimul_project_kernel<float, 1><<<grid, 512, 0, s>>>(a);
+    if (wide) timer.launch(trimul_project_kernel<float, 2>, dim3(grid), dim3(512), 0, a);
+    else timer.launch(trimul_project_kernel<float, 1>, dim3(grid), dim3(512), 0, a);
   }
   return check_launch("trimul_project");
 }
@@ -319,15 +319,15 @@ int trimul_output(const TriOutputArgs &a, int pair_dtype, int out_dtype, hipStre
   int cus = 0;
   XFH_TRY(device_cu_count(&cus));
   const dim3 grid(unsigned(balanced_grid(steps, 8, cus)));
-  KernelTimer timer("trimul_output", s);
+  KernelTimer timer("trimul_output", s, 0.0, true);
   if (pair_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    trimul_output_kernel<bf16, bf16><<<grid, 512, 0, s>>>(a);
+    timer.launch(trimul_output_kernel<bf16, bf16>, dim3(grid), dim3(512), 0, a);
   else if (pair_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    trimul_output_kernel<bf16, float><<<grid, 512, 0, s>>>(a);
+    timer.launch(trimul_output_kernel<bf16, float>, dim3(grid), dim3(512), 0, a);
   else if (pair_dtype == XFH_F32 && out_dtype == XFH_F32)
-    trimul_output_kernel<float, float><<<grid, 512, 0, s>>>(a);
+    timer.launch(trimul_output_kernel<float, float>, dim3(grid), dim3(512), 0, a);
   else
-    trimul_output_kernel<float, bf16><<<grid, 512, 0, s>>>(a);
+    timer.launch(trimul_output_kernel<float, bf16>, dim3(grid), dim3(512), 0, a);
   return check_launch("trimul_output");
 }
 
