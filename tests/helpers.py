@@ -48,6 +48,7 @@ def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
 
 def assert_parity(actual, expected, tol, what=""):
     err = rel_err(actual, expected)
+    print(f"[parity] {what}: max {err:.3e} bar {tol:.1e}", flush=True)
     assert err <= tol, f"{what}: max|diff|/rms = {err:.3e} > {tol:.1e}"
     return err
 
