@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define XFH_ABI_VERSION 8
+#define XFH_ABI_VERSION 9
 
 enum { XFH_F32 = 0, XFH_BF16 = 1, XFH_BOOL = 2 };
 enum { XFH_OK = 0, XFH_EINVAL = 1, XFH_EUNSUPPORTED = 2, XFH_EWORKSPACE = 3, XFH_EHIP = 4 };
@@ -266,6 +266,19 @@ int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t 
                    const void *w1_packed, const void *w2, int dtype,
                    void *out, int out_dtype, int accumulate,
                    void *workspace, int64_t workspace_bytes, void *stream);
+
+/* The pair transition of a Pairformer block with a single track, in place (pair += the
+ * transition of pair, bf16 [n, n, 128], hidden 512), followed by that block's attention
+ * bias of the updated pair, Linear(LN(pair)) -> packed [heads, n, align64(n)] fp32 times
+ * log2(e) with zero pad columns (the xfh_pair_attention_bias layout), written from the
+ * values the transition stores instead of a second pass over the pair. The results equal
+ * xfh_transition (accumulate = 1) followed by xfh_pair_attention_bias (fp32 out) bit for
+ * bit. 1..16 heads. Replaces pairformer.py:100 and :103-106 (xfold/nn/pairformer.py),
+ * the block's last pair update and its pair-logit projection. */
+int xfh_transition_pair_bias(void *pair, int64_t n, int64_t c, int64_t f, const float *norm_w,
+                             const float *norm_b, float eps, const void *w1_packed, const void *w2,
+                             const float *bias_ln_w, const float *bias_ln_b, float bias_eps,
+                             const void *bias_w, int64_t heads, float *packed, void *stream);
 
 /* OuterProductMean of the Evoformer's MSA stack over a contiguous msa [rows, n, c_msa] with
  * mask [rows, n] (NULL = all ones):

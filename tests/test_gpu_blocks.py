@@ -165,6 +165,23 @@ def test_pairformer_block_updates_in_place(device):
     assert p2.data_ptr() == pair.data_ptr() and s2.data_ptr() == single.data_ptr()
 
 
+def test_pairformer_block_fused_transition_logits(device, monkeypatch):
+    """The block with its pair transition and pair logits in one kernel gives the same pair
+    and single, bit for bit, as with the two kernels."""
+    from xfold_cpu_amd.nn import pairformer as P
+    announce("pairformer_block fused transition+logits", 72)
+    args = dict(n_heads=16, c_pair=128, c_single=384, n_heads_pair=4)
+    _, hip = pair_of("PairformerBlock", args, seed=5, device=device)
+    inp = pair_block_inputs(72, pad=5, seed=5)
+    outs = []
+    for fused in (True, False):
+        monkeypatch.setattr(P, "FUSE_TRANSITION_AND_LOGITS", fused)
+        pair, single = inp.pair.bfloat16().to(device), inp.single.bfloat16().to(device)
+        with torch.inference_mode(), torch.amp.autocast("cuda", dtype=torch.bfloat16):
+            outs.append(hip(pair, inp.pair_mask.to(device), single, inp.seq_mask.to(device)))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+
+
 @pytest.mark.parametrize("mode", ["fp32", "bf16-compute", "bf16"])
 def test_diffusion_transformer_batched_samples(device, mode):
     """Five samples batched in one call equal the reference's one-sample-at-a-time loop."""

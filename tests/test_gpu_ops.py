@@ -219,6 +219,35 @@ def test_pair_attention_bias(device, n, heads, pair_dtype, out_dtype):
     assert_parity_bf16(got[..., :n], want, "pair_attention_bias", floor=floor)
 
 
+@pytest.mark.parametrize("n,heads", [(1, 16), (37, 16), (64, 4), (130, 16), (257, 7)])
+def test_transition_pair_bias_fused(device, n, heads):
+    """The single-track block's pair transition with the pair logits computed in its epilogue
+    (xfh_transition_pair_bias) equals xfh_transition then xfh_pair_attention_bias bit for
+    bit: the updated pair, the packed logits and their zero pad columns (xfold/nn/pairformer.py:100-106)."""
+    from xfold_cpu_amd.nn import pairformer as P
+    from xfold_cpu_amd.nn.primitives import transition_hip
+    announce("transition_pair_bias", n, heads)
+    ref = init_module_(R.PairformerBlock(n_heads=heads, with_single=True).eval(), seed=n, ln_jitter=True)
+    block = hnn.PairformerBlock(n_heads=heads, with_single=True).eval()
+    block.load_state_dict(ref.state_dict())
+    block = block.to(device)
+    g = torch.Generator().manual_seed(n + 3 * heads)
+    pair = (torch.randn(n, n, 128, generator=g) * 2 + 0.5).bfloat16().to(device)
+    fused, split = pair.clone(), pair.clone()
+    with torch.inference_mode(), torch.amp.autocast("cuda", dtype=torch.bfloat16):
+        got = P._transition_with_logits_hip(block, fused)
+        transition_hip(block.pair_transition, split, accumulate_into=split)
+        norm = block.single_pair_logits_norm
+        want = ops.pair_attention_bias(split, norm.weight, norm.bias, norm.eps,
+                                       nh.linear_weight(block, "single_pair_logits_projection", torch.bfloat16),
+                                       owner=norm)
+    torch.cuda.synchronize()
+    assert got is not None and got.tensor.shape == want.shape == (heads, n, (n + 63) // 64 * 64)
+    assert torch.equal(fused, split), "updated pair differs"
+    assert torch.equal(got.tensor, want), f"logits differ: max {(got.tensor - want).abs().max().item()}"
+    assert bool((got.tensor[..., n:] == 0).all())
+
+
 @pytest.mark.parametrize("d", [32, 48, 64])
 @pytest.mark.parametrize("batch", [1, 3])
 def test_attention_packed_bias_bf16(device, d, batch):

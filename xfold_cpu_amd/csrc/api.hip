@@ -676,4 +676,26 @@ int xfh_transition(const void *x, int x_dtype, int64_t rows, int64_t c, int64_t 
   return gemm_nt(g, 1, dtype, out_dtype, false, s);
 }
 
+int xfh_transition_pair_bias(void *pair, int64_t n, int64_t c, int64_t f, const float *norm_w,
+                             const float *norm_b, float eps, const void *w1_packed, const void *w2,
+                             const float *bias_ln_w, const float *bias_ln_b, float bias_eps,
+                             const void *bias_w, int64_t heads, float *packed, void *stream) {
+  XFH_REQUIRE(n >= 0, "transition_pair_bias: bad size");
+  XFH_REQUIRE(c == 128 && f == 512, "transition_pair_bias: 128 pair channels and 512 hidden");
+  XFH_REQUIRE(heads > 0 && heads <= 16, "transition_pair_bias: 1..16 heads");
+  XFH_REQUIRE(n <= grid_attention_max_n(), "transition_pair_bias: more keys than the attention kernel takes");
+  XFH_REQUIRE(eps >= 0.f && bias_eps >= 0.f, "transition_pair_bias: eps must be nonnegative");
+  if (n == 0) return XFH_OK;
+  XFH_REQUIRE(pair && w1_packed && w2 && bias_w && packed, "transition_pair_bias: null tensor");
+  XFH_REQUIRE(reinterpret_cast<uintptr_t>(packed) % 16 == 0, "transition_pair_bias: packed must be 16-byte aligned");
+  TransitionArgs ta;
+  ta.x = pair; ta.rows = n * n; ta.ln_w = norm_w; ta.ln_b = norm_b; ta.eps = eps;
+  ta.w1 = static_cast<const bf16 *>(w1_packed); ta.w2 = static_cast<const bf16 *>(w2);
+  ta.out = pair; ta.accumulate = 1;
+  TransitionBias tb;
+  tb.ln_w = bias_ln_w; tb.ln_b = bias_ln_b; tb.eps = bias_eps; tb.w = static_cast<const bf16 *>(bias_w);
+  tb.packed = packed; tb.n = int(n); tb.npad = int(align_up(n, 64)); tb.heads = int(heads);
+  return transition_pair_bias(ta, tb, as_stream(stream));
+}
+
 }  // extern "C"

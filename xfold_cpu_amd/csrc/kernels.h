@@ -194,6 +194,18 @@ struct TransitionArgs {
   int accumulate;
 };
 int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStream_t s);
+// The in-place bf16 pair transition (a.x == a.out, accumulating) followed by the attention
+// bias Linear(LayerNorm(pair)) of the updated pair, computed in the transition's epilogue
+// from the values it stores: the result equals transition_fused then pair_bias (fp32 times
+// log2(e), [heads][n][npad], zero pad columns) bit for bit; heads <= 16, a.rows == n * n.
+struct TransitionBias {
+  const float *ln_w, *ln_b;
+  float eps;
+  const bf16 *w;             // [heads][128]
+  float *packed;             // [heads][n][npad]
+  int n, npad, heads;
+};
+int transition_pair_bias(const TransitionArgs &a, const TransitionBias &b, hipStream_t s);
 
 // Layouts of the triangle multiplication's contraction (c = channels, ld = contraction_ld(n)):
 //   operand (left, right): element (ch, i, t) of the per-channel [n][ld] matrices in blocks of

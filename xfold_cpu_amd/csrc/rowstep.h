@@ -267,5 +267,50 @@ __device__ __forceinline__ void o_to_operand(const float (&y)[8][4], bf16x8 (&x)
     }
 }
 
+// Swap of `hi` across the two 32-lane halves (permlane32_swap: vdst's lanes 32-63 trade
+// places with src0's lanes 0-31) or across rows 0/1 and 2/3 (permlane16_swap: vdst's odd
+// rows trade places with src0's even rows). The results pass through an empty asm, as in
+// position_sum.
+__device__ __forceinline__ void swap32(uint32_t &vdst, uint32_t &src0) {
+  const auto r = __builtin_amdgcn_permlane32_swap(vdst, src0, false, false);
+  uint32_t a = r[0], b = r[1];
+  asm volatile("" : "+v"(a), "+v"(b));
+  vdst = a;
+  src0 = b;
+}
+__device__ __forceinline__ void swap16(uint32_t &vdst, uint32_t &src0) {
+  const auto r = __builtin_amdgcn_permlane16_swap(vdst, src0, false, false);
+  uint32_t a = r[0], b = r[1];
+  asm volatile("" : "+v"(a), "+v"(b));
+  vdst = a;
+  src0 = b;
+}
+
+// One k-step of a kperm-ordered operand (lane group g holds channels 32 ks + 4 g .. +3 in
+// elements 0-3 and 32 ks + 16 + 4 g .. +3 in 4-7) into K-layout (lane group g holds
+// 32 ks + 8 g .. + 7), in place. With g = 2 hi + lo, piece a (elements 0-3 or 4-7) of lane
+// group 2 c + e belongs to lane group 2 a + c as its piece e: one swap across the halves
+// moves piece a to half a, one swap across rows moves it to row c.
+__device__ __forceinline__ void o_to_k_step(bf16x8 &x) {
+  uint4 d = __builtin_bit_cast(uint4, x);
+  swap32(d.x, d.z);                       // lower half: piece 0 of both halves,
+  swap32(d.y, d.w);                       // upper half: piece 1 of both halves
+  swap16(d.x, d.z);                       // row c: piece a of lane groups 2 c, 2 c + 1
+  swap16(d.y, d.w);
+  x = __builtin_bit_cast(bf16x8, d);
+}
+
+// O-layout tiles 2 ks and 2 ks + 1 (4 values each) as k-step ks of a kperm-ordered operand
+// (one step of o_to_operand).
+__device__ __forceinline__ bf16x8 pack_tiles(const float (&lo)[4], const float (&hi)[4]) {
+  bf16x8 x;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    x[e] = bf16(lo[e]);
+    x[4 + e] = bf16(hi[e]);
+  }
+  return x;
+}
+
 }  // namespace rowstep
 }  // namespace xfh

@@ -94,10 +94,18 @@ template <> struct RawK<float> {
 
 // RES_INIT (bf16 in place, accumulating: the pair stack's residual update): the
 // accumulators start from x itself, so the epilogue is a plain store of x + update.
-template <typename TIN, typename TOUT, bool RES_INIT>
-__global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(TransitionArgs a, int64_t total_sets) {
+// PB (with RES_INIT): the epilogue also writes the attention bias of the stored pair values
+// (pair_bias.hip's arithmetic in the same order: the bf16 values moved to K-layout by lane
+// swaps, LayerNorm, x . W^T over the 16-head tile, times log2(e)), so the pair is not read
+// again for it (xfold/nn/pairformer.py:100-106).
+template <typename TIN, typename TOUT, bool RES_INIT, bool PB>
+__global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(TransitionArgs a, TransitionBias pb,
+                                                                           int64_t total_sets) {
   __shared__ __attribute__((aligned(16))) bf16 ring[SLOTS * SLOT];
   __shared__ float lnw[C], lnb[C];
+  __shared__ __attribute__((aligned(16))) bf16 w_pb[PB ? 16 * C : 8];
+  __shared__ __attribute__((aligned(16))) float lnw_pb[PB ? C : 4], lnb_pb[PB ? C : 4];
+  static_assert(!PB || RES_INIT, "the bias epilogue follows the in-place pair update");
 
   // Contiguous range of 16-position sets for this workgroup.
   const int64_t set_begin = total_sets * blockIdx.x / gridDim.x;
@@ -149,12 +157,68 @@ __global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(Trans
       dma16(seg < 16 ? w1c : w2c, src_off[j], slot + seg * 512);
     }
   };
-  LnStage sl;
+  LnStage sl, sl_pb;
+  WeightStage<16, WAVES * 64> sw_pb;
   sl.load(a.ln_w, a.ln_b);
+  if constexpr (PB) {
+    sl_pb.load(pb.ln_w, pb.ln_b);
+    sw_pb.load([&](int r) -> const bf16 * { return r < pb.heads ? pb.w + r * C : nullptr; }, false);
+  }
   if (total_chunks > 0) issue(0);
   if (total_chunks > 1) issue(1);
   sl.store(lnw, lnb);                                // (its loads are older than the chunks')
-  __syncthreads();                                   // LayerNorm parameters
+  if constexpr (PB) {
+    sl_pb.store(lnw_pb, lnb_pb);
+    sw_pb.store(w_pb);
+  }
+  __syncthreads();                                   // LayerNorm parameters (and bias weight)
+
+  // The bias of the set whose first position is p0, from its updated values acc (every lane
+  // takes part: the lane swaps and the LayerNorm's sums cross lanes).
+  auto bias_epilogue = [&](const f32x4 (&acc)[8], int64_t p0) {
+    if constexpr (PB) {
+      bf16x8 zk[4];
+      float v[32];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const float lo[4] = {acc[2 * ks][0], acc[2 * ks][1], acc[2 * ks][2], acc[2 * ks][3]};
+        const float hi[4] = {acc[2 * ks + 1][0], acc[2 * ks + 1][1], acc[2 * ks + 1][2], acc[2 * ks + 1][3]};
+        zk[ks] = pack_tiles(lo, hi);                 // the bf16 values the pair holds
+        o_to_k_step(zk[ks]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[8 * ks + j] = static_cast<float>(zk[ks][j]);
+      }
+      bf16x8 xa[4];
+      ln_k(v, lnw_pb, lnb_pb, pb.eps, xa);
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) r = mfma16(xa[ks], weight_frag(w_pb, 0, ks), r);
+      // lane: head `pos`, positions p0 + 4 g .. + 3
+      const int h = pos;
+      const int n = pb.n;
+      if (h < pb.heads) {
+        constexpr float kLog2e = 1.4426950408889634f;
+        const int64_t q = p0 + 4 * g;
+        if (n % 4 == 0 && q + 3 < rows) {
+          const int64_t i = q / n, j = q - i * n;
+          *reinterpret_cast<float4 *>(pb.packed + (int64_t(h) * n + i) * pb.npad + j) =
+              make_float4(r[0] * kLog2e, r[1] * kLog2e, r[2] * kLog2e, r[3] * kLog2e);
+          if (j + 4 == n)
+            for (int jj = n; jj < pb.npad; ++jj) pb.packed[(int64_t(h) * n + i) * pb.npad + jj] = 0.f;
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if (q + e >= rows) continue;
+            const int64_t i = (q + e) / n, j = (q + e) - i * n;
+            float *row = pb.packed + (int64_t(h) * n + i) * pb.npad;
+            row[j] = r[e] * kLog2e;
+            if (j + 1 == n)
+              for (int jj = n; jj < pb.npad; ++jj) row[jj] = 0.f;
+          }
+        }
+      }
+    }
+  };
 
   int gc = 0;                                        // chunks consumed so far
 
@@ -251,16 +315,19 @@ __global__ __launch_bounds__(WAVES * 64, WG_PER_CU) void transition_kernel(Trans
 #pragma unroll
     for (int i = 0; i < NS; ++i) {
       const int64_t p = (base + WAVES * i) * 16 + pos;
-      if (p >= rows) continue;
       TOUT *dst = out + p * C + 4 * g;
       if constexpr (res_init) {
+        if (p < rows) {
 #pragma unroll
-        for (int t = 0; t < 8; ++t) {
-          const float o[4] = {acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]};
-          store4f<TOUT>(dst + 16 * t, o);
+          for (int t = 0; t < 8; ++t) {
+            const float o[4] = {acc[i][t][0], acc[i][t][1], acc[i][t][2], acc[i][t][3]};
+            store4f<TOUT>(dst + 16 * t, o);
+          }
         }
+        bias_epilogue(acc[i], (base + WAVES * i) * 16);
         continue;
       }
+      if (p >= rows) continue;
       Raw4<TOUT> old[8];
       if (a.accumulate) {
 #pragma unroll
@@ -304,17 +371,33 @@ int transition_fused(const TransitionArgs &a, int x_dtype, int out_dtype, hipStr
   const int grid = int(std::min<int64_t>(int64_t(cus) * WG_PER_CU, sets));
   KernelTimer timer("transition", s, 0.0, true);
   const bool in_place = a.accumulate && a.out == a.x;
+  const TransitionBias none{};
   if (x_dtype == XFH_BF16 && out_dtype == XFH_BF16 && in_place)
-    timer.launch(transition_kernel<bf16, bf16, true>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
+    timer.launch(transition_kernel<bf16, bf16, true, false>, dim3(grid), dim3(WAVES * 64), 0, a, none, sets);
   else if (x_dtype == XFH_BF16 && out_dtype == XFH_BF16)
-    timer.launch(transition_kernel<bf16, bf16, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
+    timer.launch(transition_kernel<bf16, bf16, false, false>, dim3(grid), dim3(WAVES * 64), 0, a, none, sets);
   else if (x_dtype == XFH_BF16 && out_dtype == XFH_F32)
-    timer.launch(transition_kernel<bf16, float, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
+    timer.launch(transition_kernel<bf16, float, false, false>, dim3(grid), dim3(WAVES * 64), 0, a, none, sets);
   else if (x_dtype == XFH_F32 && out_dtype == XFH_F32)
-    timer.launch(transition_kernel<float, float, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
+    timer.launch(transition_kernel<float, float, false, false>, dim3(grid), dim3(WAVES * 64), 0, a, none, sets);
   else
-    timer.launch(transition_kernel<float, bf16, false>, dim3(grid), dim3(WAVES * 64), 0, a, sets);
+    timer.launch(transition_kernel<float, bf16, false, false>, dim3(grid), dim3(WAVES * 64), 0, a, none, sets);
   return check_launch("transition");
+}
+
+int transition_pair_bias(const TransitionArgs &a, const TransitionBias &b, hipStream_t s) {
+  if (!a.accumulate || a.out != a.x || b.heads < 1 || b.heads > 16 || int64_t(b.n) * b.n != a.rows ||
+      b.npad % 64 != 0 || b.npad < b.n)
+    return fail(XFH_EINVAL, "transition_pair_bias: an in-place pair update, n * n rows, 1..16 heads, "
+                            "npad a multiple of 64 >= n");
+  if (a.rows == 0) return XFH_OK;
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const int64_t sets = ceil_div(a.rows, int64_t(16));
+  const int grid = int(std::min<int64_t>(int64_t(cus) * WG_PER_CU, sets));
+  KernelTimer timer("transition", s, 0.0, true);
+  timer.launch(transition_kernel<bf16, bf16, true, true>, dim3(grid), dim3(WAVES * 64), 0, a, b, sets);
+  return check_launch("transition_pair_bias");
 }
 
 }  // namespace xfh

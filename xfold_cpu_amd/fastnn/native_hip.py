@@ -28,7 +28,7 @@ from typing import Optional
 import torch
 
 LIBRARY_PATH = Path(__file__).resolve().parent.parent / "lib" / "libxfold_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 F32, BF16, BOOL = 0, 1, 2
 BIAS_PACKED = 3                 # bias 'dtype' of a packed fp32 block (times log2(e))
@@ -73,6 +73,7 @@ SIGNATURES = {
                                      _p, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
     "xfh_transition_workspace_size": (_i64, [_i64, _i64, _i64, _i]),
     "xfh_transition": (_i, [_p, _i, _i64, _i64, _i64, _p, _p, _f, _p, _p, _i, _p, _i, _i, _p, _i64, _p]),
+    "xfh_transition_pair_bias": (_i, [_p, _i64, _i64, _i64, _p, _p, _f, _p, _p, _p, _p, _f, _p, _i64, _p, _p]),
     "xfh_outer_product_mean_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i]),
     "xfh_outer_product_mean": (_i, [_p, _i, _p, _i, _i64, _i64, _i64, _i64, _i64, _p, _p, _f, _p, _p, _p, _f,
                                     _i, _p, _i, _i, _p, _i64, _p]),

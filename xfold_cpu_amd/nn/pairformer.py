@@ -39,6 +39,42 @@ def pair_logits_hip(block: nn.Module, pair: torch.Tensor, dtype: torch.dtype):
     return logits.permute(2, 0, 1)
 
 
+# The single-track block's pair transition and pair logits in one kernel (when the shapes
+# allow it); False runs them as two kernels, with the same results bit for bit.
+FUSE_TRANSITION_AND_LOGITS = True
+
+
+def _transition_with_logits_hip(block: nn.Module, pair: torch.Tensor) -> Optional[ops.PackedBias]:
+    """``pair += pair_transition(pair)`` and then the pair logits of the updated pair
+    (``pairformer.py:100``, ``:103-106``) in one kernel, whose epilogue computes the logits
+    from the values it stores: bf16 pair [N, N, 128], hidden 512, at most 16 heads. None
+    (nothing done) for other shapes."""
+    tr, norm = block.pair_transition, block.single_pair_logits_norm
+    proj = block.single_pair_logits_projection
+    n, c = pair.shape[0], pair.shape[-1]
+    if (pair.dtype != torch.bfloat16 or pair.dim() != 3 or pair.shape[1] != n or c != 128
+            or tr.transition2.weight.shape != (c, 512) or tr.transition1.weight.shape != (1024, c)
+            or tuple(norm.normalized_shape) != (c,) or tuple(tr.input_layer_norm.normalized_shape) != (c,)
+            or proj.weight.shape[0] > 16 or n > nh.attention_max_keys()
+            or nh.compute_dtype(pair, tr.transition1.weight, tr.transition2.weight, proj.weight) != torch.bfloat16):
+        return None
+    nh.check_gpu_inference(pair)
+    nh.check_module(tr)
+    w1 = nh.linear_weight(tr, "transition1", torch.bfloat16, "glu")
+    w2 = nh.linear_weight(tr, "transition2", torch.bfloat16)
+    nw = nh.fp32_param(tr, "norm_w", tr.input_layer_norm.weight)
+    nb = nh.fp32_param(tr, "norm_b", tr.input_layer_norm.bias)
+    wb = nh.linear_weight(block, "single_pair_logits_projection", torch.bfloat16)
+    bw = nh.fp32_param(norm, "ln_weight", norm.weight)
+    bb = nh.fp32_param(norm, "ln_bias", norm.bias)
+    heads = wb.shape[0]
+    packed = torch.empty((heads, n, (n + 63) // 64 * 64), dtype=torch.float32, device=pair.device)
+    nh.call("xfh_transition_pair_bias", nh.ptr(pair), n, c, 512, nh.ptr(nw), nh.ptr(nb),
+            float(tr.input_layer_norm.eps), nh.ptr(w1), nh.ptr(w2), nh.ptr(bw), nh.ptr(bb), float(norm.eps),
+            nh.ptr(wb.contiguous()), heads, nh.ptr(packed), nh.stream_of(pair.device))
+    return ops.PackedBias(packed)
+
+
 def pairformer_block_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.Tensor,
                          single: Optional[torch.Tensor] = None,
                          seq_mask: Optional[torch.Tensor] = None):
@@ -46,22 +82,28 @@ def pairformer_block_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.
     must be contiguous and are updated in place, as the reference's ``+=`` does."""
     if not pair.is_contiguous() or (single is not None and not single.is_contiguous()):
         raise ValueError("PairformerBlock (hip) updates pair/single in place; pass contiguous tensors")
-    _pair_updates_hip(block, pair, pair_mask)
     if not block.with_single:
+        _pair_updates_hip(block, pair, pair_mask)
         return pair
-    dtype = nh.compute_dtype(pair, block.single_pair_logits_projection.weight)
-    logits = pair_logits_hip(block, pair, dtype)
+    _pair_updates_hip(block, pair, pair_mask, transition=False)
+    logits = _transition_with_logits_hip(block, pair) if FUSE_TRANSITION_AND_LOGITS else None
+    if logits is None:
+        transition_hip(block.pair_transition, pair, accumulate_into=pair)
+        dtype = nh.compute_dtype(pair, block.single_pair_logits_projection.weight)
+        logits = pair_logits_hip(block, pair, dtype)
     self_attention_hip(block.single_attention_, single, seq_mask, logits, None, accumulate_into=single)
     transition_hip(block.single_transition, single, accumulate_into=single)
     return pair, single
 
 
-def _pair_updates_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.Tensor) -> None:
+def _pair_updates_hip(block: nn.Module, pair: torch.Tensor, pair_mask: torch.Tensor,
+                      transition: bool = True) -> None:
     triangle_multiplication_hip(block.triangle_multiplication_outgoing, pair, pair_mask, accumulate_into=pair)
     triangle_multiplication_hip(block.triangle_multiplication_incoming, pair, pair_mask, accumulate_into=pair)
     grid_self_attention_hip(block.pair_attention1, pair, pair_mask, accumulate_into=pair)
     grid_self_attention_hip(block.pair_attention2, pair, pair_mask, accumulate_into=pair)
-    transition_hip(block.pair_transition, pair, accumulate_into=pair)
+    if transition:
+        transition_hip(block.pair_transition, pair, accumulate_into=pair)
 
 
 def _require_hip_backends() -> None:
