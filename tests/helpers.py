@@ -141,12 +141,17 @@ def stored_rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     return err / rms if rms > 0 else err
 
 
-def assert_parity_bf16(actual, expected, what="", floor=None):
+def assert_parity_bf16(actual, expected, what="", floor=None, composition=False):
     """bf16-mode parity, relative to RMS(expected): RMS error <= TOL_BF16 and, with a
     floor, <= FLOOR_RMS_FACTOR x the floor's RMS error + RMS_SLACK; max error <=
     max(TOL_BF16, FLOOR_FACTOR x the max error of `floor`, the case's bf16 floor,
     MAX_SIGMAS x the floor's RMS error). For a
-    bf16 `actual` both max errors are net of half an ulp per element (stored_rel_err)."""
+    bf16 `actual` both max errors are net of half an ulp per element (stored_rel_err).
+
+    ``composition``: a deep composition (many blocks in sequence) whose bf16 floor itself
+    lies above TOL_BF16 in RMS; the flat RMS cap, a per-operator and per-block bar, is then
+    dropped and only the floor-relative RMS bound applies (the test asserts that the floor
+    is indeed above the cap, so the option cannot hide a regression of a shallow case)."""
     stored = actual.dtype == torch.bfloat16
     max_of = stored_rel_err if stored else rel_err
     rms_err = rms_rel_err(actual, expected)
@@ -155,6 +160,10 @@ def assert_parity_bf16(actual, expected, what="", floor=None):
     floor_rms = rms_rel_err(floor, expected) if floor is not None else None
     guard = max(TOL_BF16, FLOOR_FACTOR * floor_err, MAX_SIGMAS * (floor_rms or 0.0))
     rms_guard = TOL_BF16 if floor is None else min(TOL_BF16, FLOOR_RMS_FACTOR * floor_rms + RMS_SLACK)
+    if composition:
+        assert floor_rms is not None and floor_rms > TOL_BF16, (
+            f"{what}: composition bar asked for a floor within the flat cap (floor rms {floor_rms})")
+        rms_guard = FLOOR_RMS_FACTOR * floor_rms + RMS_SLACK
     ratio = f" ({rms_err / floor_rms:.2f}x)" if floor_rms else ""
     print(f"[parity] {what}: rms {rms_err:.3e} floor-rms {floor_rms if floor_rms is not None else 0.0:.3e}{ratio} "
           f"rms-guard {rms_guard:.3e} | max {max_err:.3e} floor {floor_err:.3e} guard {guard:.3e}"

@@ -449,3 +449,25 @@ def test_golden_catches_a_negative_cross_attention_mask():
         avg = avg * torch.sigmoid(module.gating_query(xq))
         wrong = module.adaptive_zero_init(avg, inputs["single_cond_q"])
     assert rel_err(wrong, outputs["out"]) > 1e-3
+
+
+def test_parity_bar_for_deep_compositions():
+    """The composition form of the bf16 bar drops only the flat RMS cap, keeps the bound of
+    1.25x the floor's RMS error, and refuses a floor that lies within the cap."""
+    import pytest
+    from tests.helpers import assert_parity_bf16
+    g = torch.Generator().manual_seed(0)
+    exact = torch.randn(20000, generator=g, dtype=torch.float64)
+    noise = torch.randn(20000, generator=g, dtype=torch.float64)
+    floor = exact + 0.04 * noise                      # a floor 4e-2 RMS from exact
+    close = exact + 0.042 * torch.roll(noise, 1)      # 1.05x the floor's RMS error
+    far = exact + 0.06 * torch.roll(noise, 1)         # 1.5x
+    assert_parity_bf16(close, exact, "close", floor=floor, composition=True)
+    with pytest.raises(AssertionError):
+        assert_parity_bf16(far, exact, "far", floor=floor, composition=True)
+    with pytest.raises(AssertionError):               # the flat cap still holds without the option
+        assert_parity_bf16(close, exact, "close, flat cap", floor=floor)
+    shallow = exact + 0.01 * noise
+    with pytest.raises(AssertionError):               # the option is refused for a shallow floor
+        assert_parity_bf16(exact + 0.011 * torch.roll(noise, 1), exact, "shallow", floor=shallow,
+                           composition=True)
