@@ -12,9 +12,11 @@ as two. One JSON line per kernel.
 ``--vendor`` adds reference points from the ROCm libraries behind torch at the same shapes,
 timed with HIP events around the call: hipBLASLt's batched GEMM on the triangle
 contraction's 128 per-channel products, torch's ``scaled_dot_product_attention`` on the
-triangle attention's shape with and without its additive bias, and a square 8192^3 bf16
-GEMM (what a library GEMM reaches of the MFMA peak on this device). They are comparisons,
-not part of the backend.
+triangle attention's shape with and without its additive bias, a square 8192^3 bf16 GEMM
+(what a library GEMM reaches of the MFMA peak on this device), and a 2 GiB device-to-device
+copy and elementwise negation (what streaming kernels reach of the HBM peak). They are comparisons, not part of
+the backend; the last two are the measured peaks the kernels' fractions can also be read
+against.
 """
 
 from __future__ import annotations
@@ -132,6 +134,13 @@ def vendor_points(n: int, reps: int, dev: torch.device, c: int = 128, heads: int
     out = torch.empty(big, big, device=dev, dtype=torch.bfloat16)
     ms = _event_ms(lambda: torch.mm(a, b, out=out), max(reps // 2, 3))
     _line("vendor: torch.mm (hipBLASLt)", f"{big}^3 bf16", ms, reps, gflop=2 * big ** 3 / 1e9)
+    del a, b, out
+    src = torch.ones(1 << 29, device=dev, dtype=torch.float32)
+    dst = torch.empty_like(src)
+    ms = _event_ms(lambda: dst.copy_(src), max(reps // 2, 3))
+    _line("vendor: Tensor.copy_", "2 GiB device to device (read + write)", ms, reps, gbytes=2 * 4 * src.numel() / 1e9)
+    ms = _event_ms(lambda: torch.neg(src, out=dst), max(reps // 2, 3))
+    _line("vendor: torch.neg", "2 GiB fp32 elementwise (read + write)", ms, reps, gbytes=2 * 4 * src.numel() / 1e9)
 
 
 def main(argv=None):
@@ -182,6 +191,15 @@ def main(argv=None):
             wl = (torch.randn(16, c, device=dev) / c ** 0.5).bfloat16()
             r = _timed(["pair_bias"], lambda: ops.pair_attention_bias(pair, w, b, 1e-5, wl), args.reps)
             _line("pair_bias_kernel", f"pair logits N={n}, 16 heads", *r["pair_bias"], *work["pair_bias"][1:])
+            # The pair transition with the single track's pair logits in its epilogue (one
+            # launch; the logits add their fp32 writes to the transition's bytes).
+            blk = init_module_(hnn.PairformerBlock(n_heads=16, c_pair=c, c_single=384, n_heads_pair=4,
+                                                   with_single=True), seed=4).to(dev).eval()
+            from .nn import pairformer
+            r = _timed(["transition"], lambda: pairformer._transition_with_logits_hip(blk, pair), args.reps)
+            npad = (n + 63) // 64 * 64
+            _line("transition_kernel + pair logits", f"pair transition with 16-head logits N={n}", *r["transition"],
+                  work["transition"][1] + 16 * n * npad * 4 / 1e9, work["transition"][2] + 2 * rows * c * 16 / 1e9)
     if args.vendor:
         del pair, mask
         with torch.inference_mode():
