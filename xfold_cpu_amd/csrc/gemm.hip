@@ -6,7 +6,8 @@
 //
 // Tiling: 128 x 128 block tile, k-step 32, 256 threads = 4 wavefronts in a 2 x 2 grid,
 // each owning a 64 x 64 sub-tile = 4 x 4 MFMA 16x16 tiles (bf16: v_mfma_f32_16x16x32_bf16;
-// fp32: 8 x v_mfma_f32_16x16x4f32 per k-step). Global -> register prefetch of the next
+// fp32: 8 x v_mfma_f32_16x16x4f32 per k-step). Problems with fewer 128 x 128 tiles than two
+// per CU take 64 x 64 tiles (32 x 32 per wavefront) instead, four times as many workgroups. Global -> register prefetch of the next
 // k-step overlaps the MFMAs of the current one; LDS rows are padded by 16 bytes so the
 // 16 rows a fragment read touches fall in distinct banks.
 #include "common.h"
@@ -16,13 +17,13 @@ namespace xfh {
 
 namespace {
 
-constexpr int BM = 128, BN = 128, BK = 32, THREADS = 256;
+constexpr int BK = 32, THREADS = 256;
 
-template <typename T> struct GemmSmem {
+template <typename T, int BT> struct GemmSmem {
   static constexpr int kChunk = 16 / sizeof(T);      // elements per 16-byte vector
   static constexpr int kPitch = BK + kChunk;          // padded LDS row (elements)
-  T a[BM * kPitch];
-  T b[BN * kPitch];
+  T a[BT * kPitch];
+  T b[BT * kPitch];
 };
 
 template <typename T> __device__ __forceinline__ typename Frag<T>::type read_frag(const T *p);
@@ -68,9 +69,11 @@ __device__ __forceinline__ float apply_epilogue(int epi, float acc, TO *c, const
   }
 }
 
-template <typename T, typename TO, bool VEC, bool GLU>
+// BT x BT block tile (BT = 128 or 64), each wavefront BT/2 x BT/2 = TW x TW MFMA tiles.
+template <typename T, typename TO, bool VEC, bool GLU, int BT>
 __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
-  typedef GemmSmem<T> Smem;
+  constexpr int BM = BT, BN = BT, WT = BT / 2, TW = WT / 16;
+  typedef GemmSmem<T, BT> Smem;
   constexpr int kChunk = Smem::kChunk;
   constexpr int kPitch = Smem::kPitch;
   constexpr int kChunksPerRow = BK / kChunk;
@@ -88,11 +91,11 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
   const T *B = static_cast<const T *>(p.B) + batch * p.sB + int64_t(n0) * p.ldb;
   const int rowsA = p.M - m0, rowsB = p.N - n0;
 
-  f32x4 acc[4][4];
+  f32x4 acc[TW][TW];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TW; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < TW; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   uint4 ra[kLoads], rb[kLoads];
   auto fetch = [&](int k0) {
@@ -121,15 +124,15 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
     stash();
     __syncthreads();
     if (k0 + BK < p.K) fetch(k0 + BK);
-    typename Frag<T>::type fa[4], fb[4];
+    typename Frag<T>::type fa[TW], fb[TW];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) fa[i] = read_frag<T>(&smem.a[(wm * 64 + i * 16 + fr) * kPitch + fk]);
+    for (int i = 0; i < TW; ++i) fa[i] = read_frag<T>(&smem.a[(wm * WT + i * 16 + fr) * kPitch + fk]);
 #pragma unroll
-    for (int j = 0; j < 4; ++j) fb[j] = read_frag<T>(&smem.b[(wn * 64 + j * 16 + fr) * kPitch + fk]);
+    for (int j = 0; j < TW; ++j) fb[j] = read_frag<T>(&smem.b[(wn * WT + j * 16 + fr) * kPitch + fk]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
+      for (int j = 0; j < TW; ++j) acc[i][j] = mfma16(fa[i], fb[j], acc[i][j]);
   }
 
   TO *C = static_cast<TO *>(p.C) + batch * p.sC;
@@ -137,16 +140,16 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
   const int col_lane = lane & 15, row_lane = (lane >> 4) * 4;
   if (GLU) {
     // Packed GLU weight: 32-column groups = 16 gate columns then the 16 matching value
-    // columns, so sub-tiles (0,1) and (2,3) of a wave hold gate/value of the same features.
+    // columns, so sub-tiles (2q, 2q + 1) of a wave hold gate/value of the same features.
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      const int f = (n0 + wn * 64) / 2 + q * 16 + col_lane;
+    for (int q = 0; q < TW / 2; ++q) {
+      const int f = (n0 + wn * WT) / 2 + q * 16 + col_lane;
       if (f >= p.glu_f) continue;
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < TW; ++i)
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int m = m0 + wm * 64 + i * 16 + row_lane + e;
+          const int m = m0 + wm * WT + i * 16 + row_lane + e;
           if (m >= p.M) continue;
           const float g = acc[i][2 * q][e], v = acc[i][2 * q + 1][e];
           C[int64_t(m) * p.ldc + f] = from_f32<TO>(siluf_(g) * v);
@@ -155,15 +158,15 @@ __global__ __launch_bounds__(THREADS) void gemm_nt_kernel(GemmArgs p) {
     return;
   }
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int n = n0 + wn * 64 + j * 16 + col_lane;
+  for (int j = 0; j < TW; ++j) {
+    const int n = n0 + wn * WT + j * 16 + col_lane;
     if (n >= p.N) continue;
     const float bias = p.bias ? p.bias[batch * p.sBias + n] : 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < TW; ++i)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int m = m0 + wm * 64 + i * 16 + row_lane + e;
+        const int m = m0 + wm * WT + i * 16 + row_lane + e;
         if (m >= p.M) continue;
         TO *c = c_element(p, C, m, n);
         const TO *a = nullptr;
@@ -185,13 +188,27 @@ int launch_typed(const GemmArgs &p, int64_t batch, bool glu, hipStream_t s) {
                    (p.sA % kChunk == 0) && (p.sB % kChunk == 0) &&
                    (reinterpret_cast<uintptr_t>(p.A) % 16 == 0) &&
                    (reinterpret_cast<uintptr_t>(p.B) % 16 == 0);
-  dim3 grid(ceil_div(p.N, BN), ceil_div(p.M, BM), batch);
+  int cus = 0;
+  XFH_TRY(device_cu_count(&cus));
+  const bool small = ceil_div(p.N, int64_t(128)) * ceil_div(p.M, int64_t(128)) * batch < 2 * int64_t(cus);
+  if (small) {
+    dim3 grid(ceil_div(p.N, 64), ceil_div(p.M, 64), batch);
+    if (glu) {
+      if (vec) gemm_nt_kernel<T, TO, true, true, 64><<<grid, THREADS, 0, s>>>(p);
+      else gemm_nt_kernel<T, TO, false, true, 64><<<grid, THREADS, 0, s>>>(p);
+    } else {
+      if (vec) gemm_nt_kernel<T, TO, true, false, 64><<<grid, THREADS, 0, s>>>(p);
+      else gemm_nt_kernel<T, TO, false, false, 64><<<grid, THREADS, 0, s>>>(p);
+    }
+    return check_launch("gemm_nt");
+  }
+  dim3 grid(ceil_div(p.N, 128), ceil_div(p.M, 128), batch);
   if (glu) {
-    if (vec) gemm_nt_kernel<T, TO, true, true><<<grid, THREADS, 0, s>>>(p);
-    else gemm_nt_kernel<T, TO, false, true><<<grid, THREADS, 0, s>>>(p);
+    if (vec) gemm_nt_kernel<T, TO, true, true, 128><<<grid, THREADS, 0, s>>>(p);
+    else gemm_nt_kernel<T, TO, false, true, 128><<<grid, THREADS, 0, s>>>(p);
   } else {
-    if (vec) gemm_nt_kernel<T, TO, true, false><<<grid, THREADS, 0, s>>>(p);
-    else gemm_nt_kernel<T, TO, false, false><<<grid, THREADS, 0, s>>>(p);
+    if (vec) gemm_nt_kernel<T, TO, true, false, 128><<<grid, THREADS, 0, s>>>(p);
+    else gemm_nt_kernel<T, TO, false, false, 128><<<grid, THREADS, 0, s>>>(p);
   }
   return check_launch("gemm_nt");
 }
@@ -201,7 +218,7 @@ int launch_typed(const GemmArgs &p, int64_t batch, bool glu, hipStream_t s) {
 int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s) {
   if (p.M == 0 || p.N == 0 || batch == 0) return XFH_OK;
   if (p.M < 0 || p.N < 0 || p.K < 0) return fail(XFH_EINVAL, "gemm: negative size");
-  if (int64_t(ceil_div(p.M, BM)) > 65535) return fail(XFH_EUNSUPPORTED, "gemm: M too large for one launch");
+  if (int64_t(ceil_div(p.M, 128)) > 65535) return fail(XFH_EUNSUPPORTED, "gemm: M too large for one launch");
   if (dtype == XFH_BF16 && (out_dtype == XFH_BF16 || out_dtype == XFH_F32) && ceil_div(p.N, 64) <= 65535 &&
       batch <= 65535 && gemm_ring_supported(p, out_dtype))
     return gemm_ring(p, batch, out_dtype, glu, s);

@@ -166,6 +166,53 @@ __global__ __launch_bounds__(256) void ln_planes(const TI *__restrict__ x, int64
   }
 }
 
+// The same through LDS for C <= kPlanesMaxC: a workgroup takes 64 rows, reads each plane's
+// 64-element run of them (coalesced), keeps the [C][64] tile in LDS for the two passes of
+// statistics (4 channel groups per row, summed in LDS) and writes the 64 rows' contiguous
+// channel vectors (coalesced), instead of one thread per row storing with a stride of C.
+constexpr int kPlaneRows = 64, kPlanesMaxC = 256;
+template <typename TI, typename TO>
+__global__ __launch_bounds__(256) void ln_planes_tiled(const TI *__restrict__ x, int64_t plane, int C,
+                                                       const float *__restrict__ w,
+                                                       const float *__restrict__ b, float eps,
+                                                       TO *__restrict__ y) {
+  constexpr int P = kPlaneRows + 1;                  // padded tile row (conflict-free transposed reads)
+  __shared__ float tile[kPlanesMaxC * P];
+  __shared__ float part[4][kPlaneRows];
+  __shared__ float mean_s[kPlaneRows], rstd_s[kPlaneRows];
+  const int64_t r0 = int64_t(blockIdx.x) * kPlaneRows;
+  const int l = threadIdx.x & 63, grp = threadIdx.x >> 6;
+  const int rows = int(plane - r0 < kPlaneRows ? plane - r0 : kPlaneRows);
+  float s = 0.f;
+  for (int c = grp; c < C; c += 4) {
+    const float v = l < rows ? to_f32(x[int64_t(c) * plane + r0 + l]) : 0.f;
+    tile[c * P + l] = v;
+    s += v;
+  }
+  part[grp][l] = s;
+  __syncthreads();
+  if (grp == 0) mean_s[l] = (part[0][l] + part[1][l] + part[2][l] + part[3][l]) / float(C);
+  __syncthreads();
+  const float mean = mean_s[l];
+  float q = 0.f;
+  for (int c = grp; c < C; c += 4) {
+    const float d = tile[c * P + l] - mean;
+    q += d * d;
+  }
+  part[grp][l] = q;                                  // (read before the previous barrier)
+  __syncthreads();
+  if (grp == 0) rstd_s[l] = rsqrtf((part[0][l] + part[1][l] + part[2][l] + part[3][l]) / float(C) + eps);
+  __syncthreads();
+  const int total = rows * C;
+  for (int i = threadIdx.x; i < total; i += 256) {
+    const int row = i / C, c = i - row * C;
+    float t = (tile[c * P + row] - mean_s[row]) * rstd_s[row];
+    if (w) t *= w[c];
+    if (b) t += b[c];
+    y[(r0 + row) * int64_t(C) + c] = from_f32<TO>(t);
+  }
+}
+
 template <typename TI, typename TO, typename TA, int MODE>
 static int launch_rows(const void *x, int64_t rows, int64_t C, const float *w, const float *b,
                        const void *scale, const void *shift, int64_t cond_rows, float eps, void *y,
@@ -230,6 +277,18 @@ int adaptive_layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, con
 int layer_norm_planes(const void *x, int xd, int64_t plane, int C, const float *w, const float *b,
                       float eps, void *y, int yd, hipStream_t s) {
   if (plane == 0) return XFH_OK;
+  if (C <= kPlanesMaxC) {
+    dim3 tiles(ceil_div(plane, int64_t(kPlaneRows)));
+    if (xd == XFH_F32 && yd == XFH_F32)
+      ln_planes_tiled<float, float><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (float *)y);
+    else if (xd == XFH_BF16 && yd == XFH_BF16)
+      ln_planes_tiled<bf16, bf16><<<tiles, 256, 0, s>>>((const bf16 *)x, plane, C, w, b, eps, (bf16 *)y);
+    else if (xd == XFH_F32 && yd == XFH_BF16)
+      ln_planes_tiled<float, bf16><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (bf16 *)y);
+    else
+      return fail(XFH_EUNSUPPORTED, "layer_norm_planes: unsupported dtypes");
+    return check_launch("layer_norm_planes");
+  }
   dim3 grid(ceil_div(plane, 256));
   if (xd == XFH_F32 && yd == XFH_F32)
     ln_planes<float, float><<<grid, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (float *)y);
