@@ -401,6 +401,25 @@ def test_triangle_multiplication(device, n, outgoing, bf16):
                  (pair.to(device), mask.to(device)), bf16, "trimul")
 
 
+@pytest.mark.parametrize("c,n", [(64, 40), (96, 33), (288, 24)])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_triangle_multiplication_other_widths(device, c, n, bf16):
+    """Pair widths off the c = 128 fast path (the generic GEMM and LayerNorm kernels): the
+    template stack's 64, an odd multiple of 32, and 288 (> 256 channels, where the
+    channel-plane LayerNorm takes its untiled form)."""
+    announce("trimul width", c, n, bf16)
+    ref, hip = pair_of("TriangleMultiplication", dict(c_pair=c, _outgoing=True), seed=c + n)
+    torch.manual_seed(c)
+    pair = torch.randn(n, n, c)
+    seq = torch.ones(n)
+    seq[-3:] = 0
+    mask = seq[:, None] * seq[None, :]
+    if bf16:
+        pair = pair.bfloat16()
+    check_module(ref, hip, hnn.triangle_multiplication_hip, (pair.float(), mask),
+                 (pair.to(device), mask.to(device)), bf16, f"trimul c={c}")
+
+
 # n = 520: enough 32-position units (520 x 17) for the 32-position projection path on a
 # 256-CU device; the smaller sizes take the 16-position path.
 @pytest.mark.parametrize("n,mask_dtype", [(33, torch.float32), (96, torch.bfloat16), (45, torch.bool),
