@@ -440,8 +440,8 @@ def cpu_c5_sample(leg):
 
 
 def cpu_baseline(cfg_name, runs=3):
-    """The reference's CPU backends restated and timed on this host (BASELINE.md protocol):
-    1 warm-up then the median of ``runs`` runs, on ``cpu_threads()`` threads. The torch leg is
+    """The reference's CPU backends restated and timed on this host: 1 warm-up then the
+    median of ``runs`` runs, on ``cpu_threads()`` threads (all cores of the affinity). The torch leg is
     oracle.restatement (the reference's torch backend); the cpp leg is oracle.cpp_port (the
     af3_kernels algorithms). ``value`` is the torch leg, in ms per Pairformer block (per
     transformer forward for C4); C3's 48-block figure is one block's time x 48."""
