@@ -94,6 +94,36 @@ def test_attention_edge_shapes(device, q_len, k_len, mask_rank, d, dtype):
     check(got, want, dtype == torch.bfloat16, "attention edges", floor)
 
 
+@pytest.mark.parametrize("k_len,pipelined", [(4096, True), (4100, False)])
+def test_attention_at_the_key_limit(device, k_len, pipelined):
+    """bf16 attention at the pipelined kernel's key limit (4096 keys: 64 key blocks, the last
+    one partly masked) and just beyond it, where the general kernel takes the call; the timer
+    of the pipelined kernel tells which one ran."""
+    from xfold_cpu_amd.fastnn import native_hip as nh
+    announce("attention key limit", k_len)
+    assert nh.attention_max_keys() == 4096
+    g = torch.Generator().manual_seed(k_len)
+    B, H, Q, d = 2, 2, 48, 32
+    q, k, v = (torch.randn(B, H, n_, d, generator=g).bfloat16() for n_ in (Q, k_len, k_len))
+    bias = torch.randn(H, Q, k_len, generator=g).bfloat16()
+    keep = torch.rand(B, k_len, generator=g) > 0.3
+    keep[:, 0] = True
+    keep[:, -40:] = False
+    def oracle():
+        return R.dot_product_attention(q.float(), k.float(), v.float(), keep, bias.float())
+    want, floor = oracle(), floor_of(oracle, stored=True)
+    nh.kernel_timing_read("mha_attention")
+    nh.set_kernel_timing(True)
+    try:
+        got = fastnn.dot_product_attention(q.to(device), k.to(device), v.to(device), keep.to(device),
+                                           bias.to(device))
+        torch.cuda.synchronize()
+    finally:
+        nh.set_kernel_timing(False)
+    assert (nh.kernel_timing_read("mha_attention")[1] > 0) == pipelined
+    check(got, want, True, f"attention {k_len} keys", floor)
+
+
 @pytest.mark.parametrize("n,samples", [(1, 1), (2, 3), (5, 1)])
 def test_diffusion_transformer_tiny(device, n, samples):
     announce("diffusion transformer tiny", n, samples)
