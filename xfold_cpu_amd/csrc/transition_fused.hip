@@ -12,10 +12,10 @@
 //     chunk land as lane g holding hidden features 8 g .. 8 g + 7: silu(gate) * value is
 //     then directly the K-layout operand of transition2, whose fp32 out^T accumulators
 //     persist across the 16 chunks. The hidden activations never leave the registers.
-// On gfx950 MFMA and VALU work of one SIMD do not overlap, and a wavefront issues at most
-// one 1 KB LDS read every ~28 cycles; the second workgroup of the CU (own barriers, so not
-// phase-locked to the first) fills the SIMDs while one waits on LDS, its chunk or a
-// SiLU -> MFMA dependency.
+// Within a chunk the SiLU depends on transition1's MFMAs and transition2's on the SiLU, so
+// a wavefront does not overlap them itself, and it issues at most one 1 KB LDS read every
+// ~28 cycles; the second workgroup of the CU (own barriers, so not phase-locked to the
+// first) fills the SIMDs while one waits on LDS, its chunk or a SiLU -> MFMA dependency.
 #include <algorithm>
 #include <type_traits>
 
