@@ -8,20 +8,17 @@
 // last k-step needs no bounds. The result goes to the blocked result layout: 16 pair
 // positions' channels contiguous.
 //
-// Two tilings, both with k-steps of 32, rows of 64 B in LDS whose 16-byte slots are
-// XOR-swizzled (slot c of row r holds chunk c ^ ((r >> 2) & 3), so the 16 rows of an MFMA
-// operand read hit distinct bank groups), one barrier per step, and R rows as the MFMA's A
-// operand (a lane ends up with four consecutive j of one i and writes them as one 8-byte
-// store):
-//   - N <= 1024 (contraction_split_kernel): 192 x 384 tiles, one workgroup of 8 wavefronts
-//     per CU, each wavefront 192 i x 48 j; L through LDS, each wavefront's private R band
-//     straight into registers (see the kernel).
-//   - N > 1024 (contraction_kernel): 192 x 192 tiles, two workgroups of 4 wavefronts per CU,
-//     each wavefront 96 x 96 (6 x 6 MFMA 16x16x32 tiles); both operand tiles go global -> LDS
-//     with global_load_lds_dwordx4 (no registers) into a 3-slot ring, one step ahead.
-// Channels are numbered so that each XCD works through a contiguous run of tiles: the
-// workgroups in flight on an XCD cover a few consecutive channels, whose k-slices share
-// 128-byte lines and DRAM pages.
+// Tiling: 192 x 384 output tiles, one workgroup of 8 wavefronts per CU (N <= 1024), or
+// 192 x 192 tiles, two workgroups of 4 wavefronts per CU; each wavefront owns 96 x 96 (6 x 6
+// MFMA 16x16x32 tiles). Per k-step of 32 both operand tiles go global -> LDS with
+// global_load_lds_dwordx4 (no registers) into a ring of 4 or 3 slots, so the loads of the
+// next 2 or 1 steps are in flight while step s is multiplied; one barrier per step. Rows
+// are 64 B in LDS with the 16-byte slots XOR-swizzled (slot c of row r holds chunk
+// c ^ ((r >> 2) & 3)), so the 16 rows of an MFMA operand read hit distinct bank groups.
+// The MFMA takes R rows as its A operand so that a lane ends up with four consecutive j
+// of one i and writes them as one 8-byte store. Channels are numbered so that each XCD
+// works through a contiguous run of tiles: the workgroups in flight on an XCD cover a few
+// consecutive channels, whose k-slices share 128-byte lines and DRAM pages.
 #include "common.h"
 #include "kernels.h"
 
@@ -61,6 +58,9 @@ template <int TBI_, int TBJ_, int WJ_, int SLOTS_, int WGS_> struct Tiling {
 };
 // 192 x 192, two independent workgroups per CU.
 using TileSquare = Tiling<192, 192, 2, 3, 2>;
+// 192 x 384, one workgroup of 8 wavefronts per CU: each R row band serves twice the
+// columns, so a k-step moves 36 instead of 48 KB of operands per CU for the same MFMAs.
+using TileWide = Tiling<192, 384, 4, 4, 1>;
 
 template <class T>
 __global__ __launch_bounds__(64 * T::W, T::WGS) void contraction_kernel(ContractionArgs a) {
@@ -183,161 +183,6 @@ __global__ __launch_bounds__(64 * T::W, T::WGS) void contraction_kernel(Contract
   }
 }
 
-// Split-operand variant for N <= 1024: 192 x 384 output tiles, one workgroup of 8 wavefronts
-// per CU, each wavefront owning all 192 rows i and its own 48 columns j (12 x 3 MFMA tiles).
-// Only L is shared, so only L goes through LDS (a 3-slot ring, 12 KB per k-step, read by
-// every wavefront); each wavefront's R band is private, and its three 1 KB R fragments per
-// k-step are plain 16-byte loads straight into registers (the blocked layout gives every lane
-// its fragment slice contiguously), two k-steps ahead. L is staged through registers too:
-// each thread loads three 8-byte pieces of L(s + 2) at step s and writes them into the ring at
-// step s + 1. Every load is a register load, so the compiler's waits count them exactly (a
-// global->LDS direct load in flight makes it wait for everything), and no direct load's LDS
-// write competes with the fragment reads.
-constexpr int kSplitSlots = 3;
-constexpr int kSplitTI = 192, kSplitTJ = 384, kSplitWJ = 48;
-constexpr int kSplitXT = kSplitWJ / 16;     // R fragments (j tiles) per wavefront: 3
-constexpr int kSplitYT = kSplitTI / 16;     // L fragments (i tiles): 12
-constexpr int kSplitSlotElems = kSplitTI * TK;
-constexpr int kSplitLPieces = kSplitTI * TK * 2 / 8 / 512;   // 8-byte pieces of L per thread: 3
-
-__global__ __launch_bounds__(512, 1) void contraction_split_kernel(ContractionArgs a) {
-  constexpr int SLOTS = kSplitSlots, XT = kSplitXT, YT = kSplitYT, SLOT_ELEMS = kSplitSlotElems;
-  constexpr int LP = kSplitLPieces;
-  __shared__ __attribute__((aligned(16))) bf16 lds[SLOTS * SLOT_ELEMS];
-  const int n = a.n, ld = a.ld;
-  const int tiles_i = (n + kSplitTI - 1) / kSplitTI, tiles_j = (n + kSplitTJ - 1) / kSplitTJ;
-  const int64_t per_channel = int64_t(tiles_i) * tiles_j;
-  const int64_t total = per_channel * a.channels;
-  const int64_t per_xcd = (total + 7) / 8;
-  const int64_t logical = (blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (logical >= total) return;
-  const int64_t ch = logical / per_channel;
-  const int tile = int(logical % per_channel);
-  const int i0 = (tile / tiles_j) * kSplitTI, j0 = (tile % tiles_j) * kSplitTJ;
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15, grp = lane >> 4;
-  const int64_t step_stride = op_step_stride(n, a.channels);
-
-  // L piece q = tid + 512 k of a k-step: row r = q / 8 of the tile (row i0 + r, clamped to
-  // n - 1: those results are not stored), 8-byte piece q % 8 of the row's 64-byte k-slice,
-  // stored in the swizzled slot ((q % 8) / 2) ^ ((r >> 2) & 3).
-  const bf16 *lsrc[LP];
-  int ldst[LP];
-#pragma unroll
-  for (int k = 0; k < LP; ++k) {
-    const int q = tid + 512 * k, r = q >> 3, h = q & 7, g = i0 + r;
-    lsrc[k] = a.left + op_offset(n, a.channels, int(ch), g < n ? g : n - 1, 0) + h * 4;
-    ldst[k] = r * TK + (((h >> 1) ^ ((r >> 2) & 3)) * 8) + (h & 1) * 4;
-  }
-  auto load_l = [&](int step, bf16x4 (&l)[LP]) {
-#pragma unroll
-    for (int k = 0; k < LP; ++k) l[k] = *reinterpret_cast<const bf16x4 *>(lsrc[k] + step * step_stride);
-  };
-  auto store_l = [&](const bf16x4 (&l)[LP], int slot) {
-#pragma unroll
-    for (int k = 0; k < LP; ++k) *reinterpret_cast<bf16x4 *>(lds + slot * SLOT_ELEMS + ldst[k]) = l[k];
-  };
-  // R fragment x of this wavefront: rows j0 + 48 wave + 16 x + col (clamped), k-chunk grp.
-  const bf16 *rsrc[XT];
-#pragma unroll
-  for (int x = 0; x < XT; ++x) {
-    const int g = j0 + wave * kSplitWJ + x * 16 + col;
-    rsrc[x] = a.right + op_offset(n, a.channels, int(ch), g < n ? g : n - 1, 0) + grp * 8;
-  }
-  auto load_r = [&](int step, bf16x8 (&r)[XT]) {
-#pragma unroll
-    for (int x = 0; x < XT; ++x) r[x] = *reinterpret_cast<const bf16x8 *>(rsrc[x] + step * step_stride);
-  };
-  const int frag = col * TK + ((grp ^ ((col >> 2) & 3)) * 8);
-
-  f32x4 acc[XT][YT];   // [x][y]: rows j (A operand = R), cols i (B operand = L)
-#pragma unroll
-  for (int x = 0; x < XT; ++x)
-#pragma unroll
-    for (int y = 0; y < YT; ++y) acc[x][y] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-  // Loads past the last k-step repeat it (their data is never used), so that every step
-  // issues the same loads and the compiler's waits need no path-dependent fallback.
-  const int steps = ld / TK, last = steps - 1;
-  bf16x4 lreg[LP];
-  bf16x8 r0[XT], r1[XT], r2[XT];
-  // (The same issue order as the steady state: R(t), then L(t + 1), R(t + 1).)
-  load_l(0, lreg);
-  store_l(lreg, 0);
-  load_r(0, r0);
-  load_l(last < 1 ? last : 1, lreg);
-  load_r(last < 1 ? last : 1, r1);
-  // Step s: L(s) is in slot s % 3 once every thread has passed the barrier; L(s + 1) goes from
-  // registers into slot (s + 1) % 3 (last read at step s - 2), then L(s + 2) and R(s + 2) are
-  // loaded, and the MFMAs of step s run on the R fragments of set `cur`.
-  auto step = [&](int s, bf16x8 (&cur)[XT], bf16x8 (&next2)[XT]) {
-    ring_barrier();
-    store_l(lreg, (s + 1) % SLOTS);
-    const int ahead = s + 2 < steps ? s + 2 : last;
-    load_l(ahead, lreg);
-    load_r(ahead, next2);
-    const bf16 *tl = lds + (s % SLOTS) * SLOT_ELEMS;
-    bf16x8 fl[4];
-#pragma unroll
-    for (int y = 0; y < 2; ++y) fl[y] = *reinterpret_cast<const bf16x8 *>(tl + y * 16 * TK + frag);
-#pragma unroll
-    for (int yp = 0; yp < YT / 2; ++yp) {
-      __builtin_amdgcn_sched_barrier(0);
-      if (yp + 1 < YT / 2) {
-#pragma unroll
-        for (int y = 2 * yp + 2; y < 2 * yp + 4; ++y)
-          fl[y & 3] = *reinterpret_cast<const bf16x8 *>(tl + y * 16 * TK + frag);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int y = 2 * yp; y < 2 * yp + 2; ++y)
-#pragma unroll
-        for (int x = 0; x < XT; ++x) acc[x][y] = mfma16(cur[x], fl[y & 3], acc[x][y]);
-    }
-  };
-  int s = 0;
-  for (; s + 3 <= steps; s += 3) {
-    step(s, r0, r2);
-    step(s + 1, r1, r0);
-    step(s + 2, r2, r1);
-  }
-  if (s < steps) step(s, r0, r2);
-  if (s + 1 < steps) step(s + 1, r1, r0);
-
-  // acc[x][y][e] = out[i = i0 + y*16 + col][j = j0 + 48 wave + x*16 + grp*4 + e].
-  auto at = [&](int64_t pos) { return a.out + res_offset(a.channels, int(ch), pos); };
-  const bool vec = (n % 4) == 0;
-#pragma unroll
-  for (int y = 0; y < YT; ++y) {
-    const int i = i0 + y * 16 + col;
-    if (i >= n) continue;
-#pragma unroll
-    for (int x = 0; x < XT; ++x) {
-      const int j = j0 + wave * kSplitWJ + x * 16 + grp * 4;
-      const int64_t pos = int64_t(i) * n + j;
-      if (vec && j + 4 <= n) {
-        bf16x4 v;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = bf16(acc[x][y][e]);
-        *reinterpret_cast<bf16x4 *>(at(pos)) = v;
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (j + e < n) *at(pos + e) = bf16(acc[x][y][e]);
-      }
-    }
-  }
-}
-
-int launch_split(const ContractionArgs &a, hipStream_t s) {
-  const int64_t total = ceil_div(a.n, kSplitTI) * ceil_div(a.n, kSplitTJ) * a.channels;
-  const int64_t grid = ceil_div(total, 8) * 8;
-  KernelTimer timer("trimul_contract", s, 2.0 * double(a.channels) * a.n * a.n * a.n, true);
-  timer.launch(contraction_split_kernel, dim3(grid), dim3(512), 0, a);
-  return check_launch("contraction");
-}
-
 template <class T> int launch(const ContractionArgs &a, hipStream_t s) {
   const int64_t total = ceil_div(a.n, T::TBI) * ceil_div(a.n, T::TBJ) * a.channels;
   const int64_t grid = ceil_div(total, 8) * 8;
@@ -346,11 +191,10 @@ template <class T> int launch(const ContractionArgs &a, hipStream_t s) {
   return check_launch("contraction");
 }
 
-// The split kernel up to N = 1024: measured (same box, libraries alternated, run alone) the
-// N=768 contraction 187-192 -> 166-178 us and N=384 28.7-29.1 -> 25.5-26.7 us against the
-// 192 x 384 tiles with both operands through LDS; at N=1536 it equals the square tile
-// (1136 against 1130 us), which stays there.
-constexpr int kSplitMaxN = 1024;
+// Wide tiles up to N = 1024: measured (same box, libraries alternated) the C2 block (N=384)
+// 0.579 -> 0.553 ms and the N=768 contraction 155 -> 152 us; at N=1536 the square tile's
+// two independent workgroups per CU are 7% faster.
+constexpr int kWideTileMaxN = 1024;
 
 }  // namespace
 
@@ -365,7 +209,7 @@ int64_t contraction_result_elems(int64_t n, int64_t channels) {
 int contraction(const ContractionArgs &a, hipStream_t s) {
   if (a.n == 0 || a.channels == 0) return XFH_OK;
   if (a.ld != contraction_ld(a.n)) return fail(XFH_EINVAL, "contraction: operand rows must be padded to 32");
-  return a.n <= kSplitMaxN ? launch_split(a, s) : launch<TileSquare>(a, s);
+  return a.n <= kWideTileMaxN ? launch<TileWide>(a, s) : launch<TileSquare>(a, s);
 }
 
 }  // namespace xfh
