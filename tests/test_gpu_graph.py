@@ -3,11 +3,13 @@
 (xfold/nn/diffusion_transformer.py:250-272) are captured once and replayed several times, with
 eager work and synchronisations between the replays; every replay must equal the eager
 result bit for bit (the kernels are deterministic and the path records no memset, host copy
-or synchronisation)."""
+or synchronisation). The replayed Pairformer block is also held to the fp32 CPU oracle
+(oracle/restatement.py) and its bf16 floor, the bar of the eager tests."""
 
 import pytest
 import torch
 
+from tests.helpers import assert_parity_bf16, floor_of, residual
 from tests.test_gpu_ops import announce, autocast, pair_of
 from xfold_cpu_amd.synthetic import pair_block_inputs
 
@@ -28,7 +30,9 @@ def capture(fn):
     return graph
 
 
-def replay_and_check(graph, reset, outputs, wants, replays=3):
+def replay_and_check(graph, reset, outputs, wants, replays=3, check=None):
+    """Replays `graph` after `reset()`; every replay's outputs must equal `wants` bit for bit
+    and pass `check(outputs)` when one is given."""
     for rep in range(replays):
         reset()
         graph.replay()
@@ -39,17 +43,32 @@ def replay_and_check(graph, reset, outputs, wants, replays=3):
         assert torch.isfinite(scratch)
         for got, want in zip(outputs, wants):
             assert torch.equal(got, want), f"replay {rep} differs from the eager result"
+        if check is not None:
+            check(outputs)
 
 
 @pytest.mark.parametrize("n", [48, 100])
 def test_pairformer_block_graph_replay(device, n):
     announce("graph pairformer_block", n)
     args = dict(n_heads=16, c_pair=128, c_single=384, n_heads_pair=4)
-    _, hip = pair_of("PairformerBlock", args, seed=n, device=device)
+    ref, hip = pair_of("PairformerBlock", args, seed=n, device=device)
     inp = pair_block_inputs(n, pad=3, seed=n)
     pair0, single0 = inp.pair.bfloat16().to(device), inp.single.bfloat16().to(device)
     pm, sm = inp.pair_mask.to(device), inp.seq_mask.to(device)
     pair, single = pair0.clone(), single0.clone()
+
+    def oracle(wrap=lambda t: t):
+        return ref(wrap(inp.pair.bfloat16().float()), inp.pair_mask, wrap(inp.single.bfloat16().float()),
+                   inp.seq_mask)
+    with torch.inference_mode():
+        want_pair_ref, want_single_ref = oracle()
+    floor_pair, floor_single = floor_of(lambda: oracle(residual))
+
+    def against_oracle(outputs):
+        got_pair, got_single = outputs
+        assert_parity_bf16(got_pair, want_pair_ref, f"graph replay PairformerBlock N={n} pair", floor=floor_pair)
+        assert_parity_bf16(got_single, want_single_ref, f"graph replay PairformerBlock N={n} single",
+                           floor=floor_single)
 
     def reset():
         pair.copy_(pair0)
@@ -64,7 +83,7 @@ def test_pairformer_block_graph_replay(device, n):
         want_pair, want_single = pair.clone(), single.clone()
         reset()
         graph = capture(block)
-        replay_and_check(graph, reset, (pair, single), (want_pair, want_single))
+        replay_and_check(graph, reset, (pair, single), (want_pair, want_single), check=against_oracle)
 
 
 def test_diffusion_transformer_graph_replay(device):
