@@ -211,15 +211,16 @@ int xfh_kernel_timing_read_work(const char *name, double *total_ms, int64_t *lau
   double total = 0.0, done = 0.0;
   int64_t count = 0;
   std::vector<TimedEvent> keep;
+  const char *error = nullptr;                 // every record of `name` is consumed, even after a failure
   for (auto &t : g_timed) {
     if (t.name != name) {
       keep.push_back(t);
       continue;
     }
-    if (hipEventSynchronize(t.stop) != hipSuccess) return fail(XFH_EHIP, "kernel_timing_read: sync failed");
     float ms = 0.f;
-    if (hipEventElapsedTime(&ms, t.start, t.stop) != hipSuccess)
-      return fail(XFH_EHIP, "kernel_timing_read: elapsed time failed");
+    if (!error && hipEventSynchronize(t.stop) != hipSuccess) error = "kernel_timing_read: sync failed";
+    if (!error && hipEventElapsedTime(&ms, t.start, t.stop) != hipSuccess)
+      error = "kernel_timing_read: elapsed time failed";
     total += ms;
     done += t.work;
     ++count;
@@ -227,6 +228,7 @@ int xfh_kernel_timing_read_work(const char *name, double *total_ms, int64_t *lau
     (void)hipEventDestroy(t.stop);
   }
   g_timed.swap(keep);
+  if (error) return fail(XFH_EHIP, error);
   *total_ms = total;
   *launches = count;
   *work = done;
