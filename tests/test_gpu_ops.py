@@ -460,6 +460,28 @@ def test_grid_self_attention(device, n, transpose, bf16):
                  (pair.to(device), mask.to(device)), bf16, "grid attention")
 
 
+@pytest.mark.parametrize("c,heads,n", [(64, 4, 40), (96, 4, 33), (128, 8, 70), (64, 2, 65), (48, 4, 37)])
+@pytest.mark.parametrize("transpose", [False, True])
+@pytest.mark.parametrize("bf16", [False, True])
+def test_grid_self_attention_other_widths(device, c, heads, n, transpose, bf16):
+    """Widths and head counts off the c = 128 / 4-head fast path: the template stack's 64
+    channels in 4 heads of 16 (xfold/nn/template.py:192-195), 24-, 16-, 32- and 12-wide
+    heads. In bf16 the attention runs in the pipelined kernel on operands repacked from the
+    projections, in fp32 in the per-query kernel."""
+    announce("grid_attention width", c, heads, n, transpose, bf16)
+    ref, hip = pair_of("GridSelfAttention", dict(c_pair=c, num_head=heads, transpose=transpose), seed=c + n)
+    torch.manual_seed(n + 3)
+    pair = torch.randn(n, n, c)
+    seq = torch.ones(n)
+    seq[-3:] = 0
+    mask = seq[:, None] * seq[None, :]
+    mask[1, 2] = 0                       # asymmetric: the ending node must not transpose it
+    if bf16:
+        pair = pair.bfloat16()
+    check_module(ref, hip, hnn.grid_self_attention_hip, (pair.float(), mask),
+                 (pair.to(device), mask.to(device)), bf16, f"grid attention c={c} h={heads}")
+
+
 def structured_pair_mask(n, seed):
     """Mask with every case the bf16 grid-attention kernel distinguishes per key block of 64:
     fully kept blocks, random holes, a row whose first block is fully masked, a row keeping

@@ -150,6 +150,9 @@ struct GridPlan {
   void *qh, *kh, *vt;
   float *bias_t;
   uint64_t *maskbits;
+  // bf16 at other widths: the pipelined attention kernel's operands (mha.hip)
+  void *mha_ws;
+  int64_t mha_bytes;
 };
 
 static bool grid_fast_path(int64_t n, int64_t c, int64_t heads, int dtype) {
@@ -173,6 +176,13 @@ static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t
   p.bias = cv.take(plane * heads * es);
   p.qkv = cv.take(plane * 3 * c * es);
   p.attn = cv.take(plane * c * es);
+  if (dtype == XFH_BF16 && c % heads == 0 && align_up(n, 64) <= grid_attention_max_n()) {
+    AttentionArgs a;
+    std::memset(&a, 0, sizeof(a));
+    a.B = n; a.H = heads; a.Q = n; a.K = n; a.D = c / heads; a.Dv = c / heads;
+    p.mha_bytes = mha_workspace_size(a);
+    if (p.mha_bytes > 0) p.mha_ws = cv.take(p.mha_bytes);
+  }
   return cv.used;
 }
 
@@ -629,7 +639,10 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   a.bias = p.bias; a.bias_dtype = dtype;
   a.bs[0] = 0; a.bs[1] = 1; a.bs[2] = n * heads; a.bs[3] = heads;
   a.scale = 1.0f / std::sqrt(float(dh));
-  XFH_TRY(attention(a, dtype, s));
+  // bf16: the pipelined attention kernel on operands repacked from the projections (the
+  // per-query kernel of attention.hip keeps fp32 and the shapes it does not take).
+  if (p.mha_ws && mha_supported(a, dtype)) XFH_TRY(mha(a, p.mha_ws, p.mha_bytes, s));
+  else XFH_TRY(attention(a, dtype, s));
   // attn <- sigmoid(LN(z) Wgate^T) * attn, in place.
   g = gemm_args(p.normed, c, gating_w, c, p.attn, c, plane, c, c);
   g.epi = XFH_EPI_SIGMOID_MUL_AUX; g.aux = p.attn; g.ldaux = c;
