@@ -145,7 +145,7 @@ static int64_t trimul_carve(Carver &cv, TriMulPlan &p, int64_t n, int64_t c, int
 
 // ------------------------------------------------------------------ grid self-attention
 struct GridPlan {
-  void *normed, *bias, *qkv, *attn;
+  void *normed, *bias, *qkv, *wcat, *attn;
   // fast bf16 path (c = 128, 4 heads x 32)
   void *qh, *kh, *vt;
   float *bias_t;
@@ -175,6 +175,7 @@ static int64_t grid_carve(Carver &cv, GridPlan &p, int64_t n, int64_t c, int64_t
   p.normed = cv.take(plane * c * es);
   p.bias = cv.take(plane * heads * es);
   p.qkv = cv.take(plane * 3 * c * es);
+  p.wcat = cv.take(3 * c * c * es);
   p.attn = cv.take(plane * c * es);
   if (dtype == XFH_BF16 && c % heads == 0 && align_up(n, 64) <= grid_attention_max_n()) {
     AttentionArgs a;
@@ -616,10 +617,18 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   XFH_TRY(layer_norm_rows(pair, pair_dtype, plane, c, norm_w, norm_b, eps, p.normed, dtype, s));
   GemmArgs g = gemm_args(p.normed, c, bias_w, c, p.bias, heads, plane, heads, c);
   XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
-  const void *ws[3] = {q_w, k_w, v_w};
-  for (int i = 0; i < 3; ++i) {
-    g = gemm_args(p.normed, c, ws[i], c, static_cast<char *>(p.qkv) + i * c * es, 3 * c, plane, c, c);
+  // [q | k | v] = LN(z) [Wq; Wk; Wv]^T in one GEMM: the normalised pair is read once for the
+  // three projections (each output column is the same dot product as in a GEMM of its own).
+  const void *wsrc[4] = {q_w, k_w, v_w, nullptr};
+  const int64_t wrows[4] = {c, c, c, 0};
+  if (stack_rows(p.wcat, wsrc, wrows, c, int(es), s) == XFH_OK) {
+    g = gemm_args(p.normed, c, p.wcat, c, p.qkv, 3 * c, plane, 3 * c, c);
     XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+  } else {                                           // weights not 16-byte stackable
+    for (int i = 0; i < 3; ++i) {
+      g = gemm_args(p.normed, c, wsrc[i], c, static_cast<char *>(p.qkv) + i * c * es, 3 * c, plane, c, c);
+      XFH_TRY(gemm_nt(g, 1, dtype, dtype, false, s));
+    }
   }
   AttentionArgs a;
   std::memset(&a, 0, sizeof(a));

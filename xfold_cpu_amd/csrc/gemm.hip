@@ -213,6 +213,16 @@ int launch_typed(const GemmArgs &p, int64_t batch, bool glu, hipStream_t s) {
   return check_launch("gemm_nt");
 }
 
+// Up to four row-major matrices stacked into dst (a GEMM's B operand built from separate
+// Linear weights): thread = 16 bytes of dst.
+__global__ void stack_rows_kernel(char *__restrict__ dst, const char *s0, const char *s1, const char *s2,
+                                  const char *s3, int64_t b1, int64_t b2, int64_t b3, int64_t total) {
+  const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 16;
+  if (i >= total) return;
+  const char *src = i < b1 ? s0 + i : i < b2 ? s1 + (i - b1) : i < b3 ? s2 + (i - b2) : s3 + (i - b3);
+  *reinterpret_cast<uint4 *>(dst + i) = *reinterpret_cast<const uint4 *>(src);
+}
+
 }  // namespace
 
 int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s) {
@@ -257,6 +267,21 @@ int glu_pack(const void *w, int64_t f, int64_t k, int dtype, void *packed, hipSt
   else
     return fail(XFH_EUNSUPPORTED, "glu_pack: dtype must be f32 or bf16");
   return check_launch("glu_pack");
+}
+
+int stack_rows(void *dst, const void *const src[4], const int64_t rows[4], int64_t cols, int es, hipStream_t s) {
+  const int64_t b1 = rows[0] * cols * es, b2 = b1 + rows[1] * cols * es, b3 = b2 + rows[2] * cols * es;
+  const int64_t total = b3 + rows[3] * cols * es;
+  for (int i = 0; i < 4; ++i)
+    if (rows[i] && reinterpret_cast<uintptr_t>(src[i]) % 16)
+      return fail(XFH_EUNSUPPORTED, "stack_rows: sources must be 16-byte aligned");
+  if (b1 % 16 || b2 % 16 || b3 % 16 || total % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return fail(XFH_EUNSUPPORTED, "stack_rows: matrices must be multiples of 16 bytes");
+  if (total == 0) return XFH_OK;
+  stack_rows_kernel<<<dim3(unsigned(ceil_div(total / 16, 256))), 256, 0, s>>>(
+      static_cast<char *>(dst), static_cast<const char *>(src[0]), static_cast<const char *>(src[1]),
+      static_cast<const char *>(src[2]), static_cast<const char *>(src[3]), b1, b2, b3, total);
+  return check_launch("stack_rows");
 }
 
 }  // namespace xfh

@@ -54,6 +54,9 @@ template <typename TO> __device__ __forceinline__ TO *c_element(const GemmArgs &
 }
 
 int gemm_nt(const GemmArgs &p, int64_t batch, int dtype, int out_dtype, bool glu, hipStream_t s);
+// dst = the rows of up to four row-major matrices of `cols` elements (es bytes each), stacked
+// (16-byte aligned sources, each a multiple of 16 bytes; rows[i] = 0 skips src[i]).
+int stack_rows(void *dst, const void *const src[4], const int64_t rows[4], int64_t cols, int es, hipStream_t s);
 // bf16-input GEMM with a direct-load LDS ring (gemm_ring.hip); gemm_nt routes to it when
 // gemm_ring_supported (k a multiple of 32, 16-byte aligned operand rows, 4-aligned output).
 bool gemm_ring_supported(const GemmArgs &p, int out_dtype);

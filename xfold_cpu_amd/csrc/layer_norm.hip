@@ -170,14 +170,16 @@ __global__ __launch_bounds__(256) void ln_planes(const TI *__restrict__ x, int64
 // 64-element run of them (coalesced), keeps the [C][64] tile in LDS for the two passes of
 // statistics (4 channel groups per row, summed in LDS) and writes the 64 rows' contiguous
 // channel vectors (coalesced), instead of one thread per row storing with a stride of C.
+// The tile is sized for at most MAXC channels (64, 128 or 256), so narrow pairs keep more
+// workgroups per CU in flight (C = 64: 16.6 KB each).
 constexpr int kPlaneRows = 64, kPlanesMaxC = 256;
-template <typename TI, typename TO>
+template <typename TI, typename TO, int MAXC>
 __global__ __launch_bounds__(256) void ln_planes_tiled(const TI *__restrict__ x, int64_t plane, int C,
                                                        const float *__restrict__ w,
                                                        const float *__restrict__ b, float eps,
                                                        TO *__restrict__ y) {
   constexpr int P = kPlaneRows + 1;                  // padded tile row (conflict-free transposed reads)
-  __shared__ float tile[kPlanesMaxC * P];
+  __shared__ float tile[MAXC * P];
   __shared__ float part[4][kPlaneRows];
   __shared__ float mean_s[kPlaneRows], rstd_s[kPlaneRows];
   const int64_t r0 = int64_t(blockIdx.x) * kPlaneRows;
@@ -274,20 +276,28 @@ int adaptive_layer_norm_rows(const void *x, int xd, int64_t rows, int64_t C, con
   return fail(XFH_EUNSUPPORTED, "adaptive_layer_norm: aux dtype must be f32 or bf16");
 }
 
+template <int MAXC>
+static int launch_planes_tiled(const void *x, int xd, int64_t plane, int C, const float *w, const float *b,
+                               float eps, void *y, int yd, dim3 tiles, hipStream_t s) {
+  if (xd == XFH_F32 && yd == XFH_F32)
+    ln_planes_tiled<float, float, MAXC><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (float *)y);
+  else if (xd == XFH_BF16 && yd == XFH_BF16)
+    ln_planes_tiled<bf16, bf16, MAXC><<<tiles, 256, 0, s>>>((const bf16 *)x, plane, C, w, b, eps, (bf16 *)y);
+  else if (xd == XFH_F32 && yd == XFH_BF16)
+    ln_planes_tiled<float, bf16, MAXC><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (bf16 *)y);
+  else
+    return fail(XFH_EUNSUPPORTED, "layer_norm_planes: unsupported dtypes");
+  return check_launch("layer_norm_planes");
+}
+
 int layer_norm_planes(const void *x, int xd, int64_t plane, int C, const float *w, const float *b,
                       float eps, void *y, int yd, hipStream_t s) {
   if (plane == 0) return XFH_OK;
   if (C <= kPlanesMaxC) {
     dim3 tiles(ceil_div(plane, int64_t(kPlaneRows)));
-    if (xd == XFH_F32 && yd == XFH_F32)
-      ln_planes_tiled<float, float><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (float *)y);
-    else if (xd == XFH_BF16 && yd == XFH_BF16)
-      ln_planes_tiled<bf16, bf16><<<tiles, 256, 0, s>>>((const bf16 *)x, plane, C, w, b, eps, (bf16 *)y);
-    else if (xd == XFH_F32 && yd == XFH_BF16)
-      ln_planes_tiled<float, bf16><<<tiles, 256, 0, s>>>((const float *)x, plane, C, w, b, eps, (bf16 *)y);
-    else
-      return fail(XFH_EUNSUPPORTED, "layer_norm_planes: unsupported dtypes");
-    return check_launch("layer_norm_planes");
+    if (C <= 64) return launch_planes_tiled<64>(x, xd, plane, C, w, b, eps, y, yd, tiles, s);
+    if (C <= 128) return launch_planes_tiled<128>(x, xd, plane, C, w, b, eps, y, yd, tiles, s);
+    return launch_planes_tiled<kPlanesMaxC>(x, xd, plane, C, w, b, eps, y, yd, tiles, s);
   }
   dim3 grid(ceil_div(plane, 256));
   if (xd == XFH_F32 && yd == XFH_F32)
