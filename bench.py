@@ -38,7 +38,7 @@ PEAK_HBM_GBS = 8000.0
 
 
 # (timed steps, warm-up steps) per configuration; a step is one forward of the workload.
-DEFAULT_STEPS = {"C1": (200, 50), "C2": (200, 50), "C3": (5, 2), "C4": (10, 3), "C5": (20, 5)}
+DEFAULT_STEPS = {"C1": (200, 50), "C2": (200, 50), "C3": (5, 2), "C4": (10, 3), "C5": (20, 5), "T768": (20, 5)}
 
 
 def parse():
@@ -47,7 +47,7 @@ def parse():
     p.add_argument("--steps", type=int, default=None,
                    help="timed steps (default per config: enough to reach steady clocks)")
     p.add_argument("--warmup", type=int, default=None)
-    p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5"])
+    p.add_argument("--config", default="C2", choices=["C1", "C2", "C3", "C4", "C5", "T768"])
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-c3", action="store_true",
                    help="with the default C2 configuration, skip the 48-block C3 trunk timed beside it")
@@ -91,13 +91,14 @@ def build_workload(cfg_name, device):
     if cfg["kind"] in ("pair_block", "trunk"):
         blocks = cfg.get("blocks", 1)
         with_single = cfg["with_single"]
+        c_pair, factor = cfg.get("c_pair", 128), cfg.get("factor", 4)
         mods = []
         for b in range(blocks):
-            m = hnn.PairformerBlock(n_heads=16, c_pair=128, c_single=384, n_heads_pair=4,
-                                    with_single=with_single).eval()
+            m = hnn.PairformerBlock(n_heads=16, c_pair=c_pair, c_single=384, n_heads_pair=4,
+                                    with_single=with_single, num_intermediate_factor=factor).eval()
             init_module_(m, seed=b)
             mods.append(m.to(device))
-        inp = pair_block_inputs(cfg["n"], pad=cfg["pad"], random_pad=cfg["random_pad"], seed=0,
+        inp = pair_block_inputs(cfg["n"], c_pair=c_pair, pad=cfg["pad"], random_pad=cfg["random_pad"], seed=0,
                                 with_single=with_single)
         dt = torch.bfloat16 if bf16 else torch.float32
         pair0 = inp.pair.to(dt).to(device)
@@ -116,7 +117,8 @@ def build_workload(cfg_name, device):
         workload = dict(workload=f"{cfg_name}: {blocks} Pairformer block(s), N={cfg['n']}, "
                                  f"{'single track, ' if with_single else 'pair stack, '}"
                                  f"{cfg['pad']} padded tokens", n_tokens=cfg["n"], blocks=blocks,
-                        c_pair=128, heads_pair="4x32", pair_transition="128->2x512->128")
+                        c_pair=c_pair, heads_pair=f"4x{c_pair // 4}",
+                        pair_transition=f"{c_pair}->2x{factor * c_pair}->{c_pair}")
         return step, blocks, workload, cfg
     # diffusion transformer
     m = hnn.DiffusionTransformer().eval()
@@ -293,6 +295,48 @@ def diffusion_roofline(step, cfg_name, steps):
             "flops_per_launch": round(flops / g["launches"]),
             "shape": "per block: [5*768, 768] x 768->3072 (q, k, v, gate), 768->768 (AdaLNZero), "
                      "768->3072 (GLU), 1536->768; plus the batched conditioning Linears"}, kernels
+
+
+WIDTH_TIMERS = ("mha_attention", "gemm_ring", "layer_norm")
+
+
+def width_roofline(step, n, steps):
+    """A pair block off the 128-channel fast path (the template stack's): the timed kernels'
+    average launch time per block and their declared FLOP rates; the roofline object is the
+    attention (the pipelined kernel on repacked operands, 4 B H N^2 Dv FLOPs per launch)."""
+    import torch
+    from xfold_cpu_amd.fastnn import native_hip
+
+    native_hip.set_kernel_timing(True)
+    try:
+        step()                                        # dropped: a process's first event records read high
+        torch.cuda.synchronize()
+        for name in WIDTH_TIMERS:
+            native_hip.kernel_timing_read_work(name)
+        for _ in range(steps):
+            step()
+        torch.cuda.synchronize()
+    finally:
+        native_hip.set_kernel_timing(False)
+    kernels = {}
+    for name in WIDTH_TIMERS:
+        total_ms, launches, work = native_hip.kernel_timing_read_work(name)
+        if not launches:
+            continue
+        rec = dict(avg_us=round(total_ms / launches * 1e3, 2), launches=launches,
+                   us_per_block=round(total_ms / steps * 1e3, 1))
+        if work:
+            tflops = work / (total_ms * 1e-3) / 1e12
+            rec.update(tflops=round(tflops, 1), mfma_frac=round(tflops / PEAK_BF16_TFLOPS, 4))
+        kernels[name + "_kernel"] = rec
+    a = kernels.get("mha_attention_kernel")
+    if a is None or "tflops" not in a:
+        return None, kernels
+    return {"kernel": "grid_attention_kernel on repacked operands (mha_attention)", "bound": "mfma",
+            "achieved": a["tflops"], "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": a["mfma_frac"], "traffic": None, "traffic_source": "no counter record for this configuration",
+            "avg_launch_ms": round(a["avg_us"] / 1e3, 4), "launches": a["launches"],
+            "shape": f"B={n} H=4 Q=K={n} D=16 (padded to 32) bf16"}, kernels
 
 
 def host_cpu():
@@ -541,7 +585,10 @@ def run_config(cfg_name, steps, warmup, device, graph=False, precondition_s=0.0)
     ms_step = start.elapsed_time(stop) / steps
     log(f"{cfg_name} timed {steps} steps: {ms_step:.3f} ms/step (wall {wall:.2f} s)")
     roof, kernels = None, None
-    if cfg["kind"] != "diffusion":
+    if cfg.get("c_pair", 128) != 128:
+        roof, kernels = width_roofline(step, cfg["n"], max(1, min(steps, 10)))
+        log(f"{cfg_name} roofline: {roof}")
+    elif cfg["kind"] != "diffusion":
         roof, kernels = kernel_roofline(step, cfg_name, cfg["n"], max(1, min(steps, 10)))
         log(f"{cfg_name} roofline: {roof}")
     else:
@@ -600,7 +647,9 @@ def main():
             torch.cuda.empty_cache()
 
     base = None
-    if not args.no_cpu_baseline:
+    if args.config == "T768":
+        log("cpu baseline: not measured for the template block")
+    elif not args.no_cpu_baseline:
         log("cpu baseline (restatements on host cores)")
         base = cpu_baseline(args.config)
         log(f"cpu baseline: {base}")

@@ -137,4 +137,8 @@ CONFIGS = {
     "C3": dict(kind="trunk", n=768, dtype="bf16", pad=77, random_pad=False, with_single=True, blocks=48),
     "C4": dict(kind="diffusion", n=768, dtype="bf16", samples=5, blocks=24),
     "C5": dict(kind="pair_block", n=1536, dtype="bf16", pad=77, random_pad=True, with_single=False),
+    # The template stack's block (xfold/nn/template.py:192-195): 64 pair channels, 4 heads of
+    # 16, transition factor 2; not a BASELINE configuration (bench.py --config T768).
+    "T768": dict(kind="pair_block", n=768, dtype="bf16", pad=77, random_pad=False, with_single=False,
+                 c_pair=64, factor=2),
 }
