@@ -54,18 +54,27 @@ __global__ __launch_bounds__(256) void opm_operands_kernel(const T *__restrict__
 }
 
 // kt[k] = 1e9 * (max over s of mask[s][k] - 1) (0 without a mask): the additive key term of
-// xfold/nn/attention.py:129.
-__global__ void msa_key_term_kernel(const void *__restrict__ mask, int mask_dtype, int rows, int n,
-                                    float *__restrict__ kt) {
-  const int k = blockIdx.x * blockDim.x + threadIdx.x;
-  if (k >= n) return;
-  if (!mask) {
-    kt[k] = 0.f;
-    return;
-  }
+// xfold/nn/attention.py:129. Workgroup = 64 keys; its 16 wavefronts take every 16th MSA row
+// (independent loads, several in flight per lane), then combine their maxima through LDS.
+constexpr int kKeyTermWaves = 16;
+__global__ __launch_bounds__(64 * kKeyTermWaves) void msa_key_term_kernel(const void *__restrict__ mask,
+                                                                         int mask_dtype, int rows, int n,
+                                                                         float *__restrict__ kt) {
+  __shared__ float part[kKeyTermWaves][64];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int k = blockIdx.x * 64 + lane;
   float m = -__builtin_inff();
-  for (int s = 0; s < rows; ++s) m = fmaxf(m, load_any(mask, mask_dtype, int64_t(s) * n + k));
-  kt[k] = 1e9f * (m - 1.0f);
+  if (mask && k < n) {
+#pragma unroll 4
+    for (int s = wave; s < rows; s += kKeyTermWaves) m = fmaxf(m, load_any(mask, mask_dtype, int64_t(s) * n + k));
+  }
+  part[wave][lane] = m;
+  __syncthreads();
+  if (wave == 0 && k < n) {
+#pragma unroll
+    for (int w = 1; w < kKeyTermWaves; ++w) m = fmaxf(m, part[w][lane]);
+    kt[k] = mask ? 1e9f * (m - 1.0f) : 0.f;
+  }
 }
 
 // One wavefront per (head h, query q): w[h][q][k] = softmax over k < n of
@@ -296,7 +305,8 @@ int xfh_msa_attention(const void *msa, int msa_dtype, const void *mask, int mask
     logit_dtype = dtype; sh = 1; sq = n * heads; sk = heads;
     scale = 1.0f;
   }
-  msa_key_term_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, s>>>(mask, mask_dtype, int(rows), int(n), p.kt);
+  msa_key_term_kernel<<<dim3(unsigned(ceil_div(n, 64))), 64 * kKeyTermWaves, 0, s>>>(mask, mask_dtype, int(rows),
+                                                                                      int(n), p.kt);
   XFH_TRY(check_launch("msa_key_term"));
   const dim3 sgrid(unsigned(ceil_div(heads * n, 4)));
   if (dtype == XFH_BF16)
