@@ -59,7 +59,8 @@ typedef __attribute__((address_space(1))) void global_void;
 typedef __attribute__((address_space(3))) void lds_void;
 
 // Workgroup shape: R batch rows, W wavefronts, TQ tiles of 16 queries per wavefront, head
-// dim D (32 or 64; smaller heads are zero-padded).
+// dim D (16, 32 or 64; other heads are zero-padded to the next). At D = 16 the Q.K^T MFMA
+// takes its k = 16 .. 31 half as zeros (the lanes of k-groups 2 and 3 supply zero fragments).
 template <int R_, int W_, int TQ_, int D_> struct Shape {
   static constexpr int R = R_, W = W_, TQ = TQ_, D = D_;
   static constexpr int Q = 16 * TQ * W;                     // queries per workgroup
@@ -70,19 +71,19 @@ template <int R_, int W_, int TQ_, int D_> struct Shape {
   static constexpr int KPIECES = D / 8, PIECES = 2 * KPIECES; // 1 KB direct loads per row
   static constexpr int KPP = 512 / D;                       // keys per K piece
   static constexpr int DT = D / 16;                         // output tiles (+ 1 denominator)
-  static constexpr int KS = D / 32;                         // k-steps of Q.K^T
+  static constexpr int KS = D == 16 ? 1 : D / 32;           // k-steps of Q.K^T
   static constexpr int BLOCKS = (8 / W) * (R == 1 ? 2 : 1); // workgroups per CU
-  static_assert(D == 32 || D == 64, "head dim 32 or 64");
+  static_assert(D == 16 || D == 32 || D == 64, "head dim 16, 32 or 64");
   static_assert(W >= R, "wavefront r writes row r's mask row");
   static_assert(PIECES % W == 0, "each wavefront loads the same number of pieces of a row");
 };
 using GridShape = Shape<4, 4, 1, 32>;
 
 // K slot swizzle: 16-byte slot s of key j holds chunk s ^ kswz(j), so that the 16 keys of an
-// MFMA operand read (one chunk each) hit distinct bank groups for 64-byte (D = 32) and
-// 128-byte (D = 64) rows.
+// MFMA operand read (one chunk each) hit distinct bank groups for 32-byte (D = 16), 64-byte
+// (D = 32) and 128-byte (D = 64) rows.
 template <int D> __host__ __device__ constexpr int kswz(int key) {
-  return D == 32 ? (key >> 2) & 3 : (key >> 1) & 7;
+  return D == 16 ? (key >> 3) & 1 : D == 32 ? (key >> 2) & 3 : (key >> 1) & 7;
 }
 
 __device__ __forceinline__ uint32_t xcd_logical(uint32_t physical, uint32_t per_xcd) {
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       for (int ks = 0; ks < KS; ++ks) {
         bf16x8 z = {};
         qf[r][tq][ks] = z;
-        if (b < a.B && q < a.Nq)
+        if (b < a.B && q < a.Nq && (D != 16 || grp < 2))
           qf[r][tq][ks] = *reinterpret_cast<const bf16x8 *>(a.q + ((int64_t(b) * a.H + h) * a.Nq + q) * D + ks * 32 + grp * 8);
       }
 #pragma unroll
@@ -314,7 +315,8 @@ __global__ __launch_bounds__(S::T, S::BLOCKS) void grid_attention_kernel(GridAtt
       bf16x8 kf[KS];
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        kf[ks] = *reinterpret_cast<const bf16x8 *>(kr + (kt * 16 + col) * D + kslot[ks]);
+        kf[ks] = *reinterpret_cast<const bf16x8 *>(D == 16 && grp >= 2 ? mzero
+                                                                       : kr + (kt * 16 + col) * D + kslot[ks]);
 #pragma unroll
       for (int tq = 0; tq < TQ; ++tq) {
         s[tq][kt] = mfma16(kf[0], qf[r][tq][0], bias[tq][kt]);
@@ -550,7 +552,14 @@ int mha_attention(const GridAttentionArgs &a, int d, hipStream_t s) {
   if (d == 64)
     return a.bias_bf16 ? launch<Shape<1, 8, 1, 64>, bf16>(a, "mha_attention", s)
                        : launch<Shape<1, 8, 1, 64>>(a, "mha_attention", s);
-  return fail(XFH_EUNSUPPORTED, "mha_attention: head dim must be 32 or 64");
+  if (d == 16) {
+    if (a.B == 1)
+      return a.bias_bf16 ? launch<Shape<1, 4, 1, 16>, bf16>(a, "mha_attention", s)
+                         : launch<Shape<1, 4, 1, 16>>(a, "mha_attention", s);
+    return a.bias_bf16 ? launch<Shape<4, 4, 1, 16>, bf16>(a, "mha_attention", s)
+                       : launch<Shape<4, 4, 1, 16>>(a, "mha_attention", s);
+  }
+  return fail(XFH_EUNSUPPORTED, "mha_attention: head dim must be 16, 32 or 64");
 }
 
 int64_t grid_attention_pad(int64_t n) { return grid_attention_pad_(n); }

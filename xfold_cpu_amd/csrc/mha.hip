@@ -1,6 +1,6 @@
 // dot_product_attention (xfold/fastnn/attention.py:45-66) on the triangle-attention kernel
 // (grid_attention.hip): one preparation launch turns the caller's strided q, k, v, bias and
-// mask into that kernel's layouts, then the kernel runs at head dim 32 or 64.
+// mask into that kernel's layouts, then the kernel runs at head dim 16, 32 or 64.
 //
 // Preparation (one launch; each part takes its own range of workgroups):
 //   0  q  [B][H][Nq][D]   = q * scale * log2(e), zero for d >= Dqk
@@ -153,7 +153,7 @@ __global__ void mha_prepare_kernel(MhaPrep p) {
   }
 }
 
-int padded_dim(int64_t d) { return d <= 32 ? 32 : d <= 64 ? 64 : 0; }
+int padded_dim(int64_t d) { return d <= 16 ? 16 : d <= 32 ? 32 : d <= 64 ? 64 : 0; }
 
 struct MhaPlan {
   int D;
