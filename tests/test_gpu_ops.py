@@ -318,7 +318,8 @@ def test_attention_reference_cases(device, mask_rank, batched, dtype):
 
 
 @pytest.mark.parametrize("shape", [(3, 4, 37, 37, 32), (1, 16, 100, 100, 24), (2, 16, 70, 70, 48),
-                                   (2, 3, 65, 130, 64), (1, 1, 1, 1, 16)])
+                                   (2, 3, 65, 130, 64), (1, 1, 1, 1, 16), (1, 4, 50, 77, 16),
+                                   (5, 2, 33, 70, 8)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_attention_shapes_masks_and_fully_masked_rows(device, shape, dtype):
     B, H, Q, K, D = shape
