@@ -728,7 +728,7 @@ def test_diffusion_transition(device, bf16):
 def _ring_config(run):
     """Runs ``run`` with kernel timing on and returns the gemm_ring configuration it took
     (the library records each launch under "gemm_ring.<tile>[+xcd]")."""
-    names = [f"gemm_ring.{t}{x}" for t in ("mid", "narrow", "shallow", "shallow_narrow", "xwide")
+    names = [f"gemm_ring.{t}{x}" for t in ("mid", "narrow", "shallow", "shallow_narrow", "xwide", "skinny")
              for x in ("", "+xcd")]
     for name in names:
         nh.kernel_timing_read(name)
@@ -753,6 +753,8 @@ def _ring_config(run):
     ("linear", 300, 96, 200, 1, "shallow_narrow"),
     ("batched", 768, 384, 768, 4, "narrow"),
     ("batched", 512, 768, 2304, 4, "mid"),
+    ("linear", 150000, 64, 256, 1, "skinny+xcd"),     # k = 64 over many tiles (64-channel pairs)
+    ("glu", 150000, 64, 128, 1, "skinny"),
 ])
 def test_gemm_ring_configurations(device, kind, m, k, n, batch, config):
     """Every gemm_ring tile configuration, at shapes that select it on a 256-CU MI355X,

@@ -437,6 +437,7 @@ using RingNarrow = Ring<64, 64, 3, 2>;    // N <= 64, or too few workgroups othe
 using RingShallow = Ring<128, 32, 4, 2>;  // k % 64 != 0
 using RingShallowNarrow = Ring<64, 32, 4, 2>;
 using RingXWide = Ring<192, 64, 2, 2>;     // 1.5x-width tiles: one round where 96 needs two
+using RingSkinny = Ring<64, 64, 2, 3>;     // k = 64 (one step) over many tiles: three workgroups per CU
 
 template <class G>
 int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStream_t s, KernelTimer &timer) {
@@ -474,7 +475,7 @@ int launch_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipSt
   return check_launch("gemm_ring");
 }
 
-enum class RingPick { Mid, Narrow, Shallow, ShallowNarrow, XWide };
+enum class RingPick { Mid, Narrow, Shallow, ShallowNarrow, XWide, Skinny };
 
 // Tile width: the 64-column tile (the only one with a 3-stage ring at two workgroups per
 // CU) unless the grid then needs more rounds of workgroups than a wider tile would, rounds
@@ -484,10 +485,15 @@ enum class RingPick { Mid, Narrow, Shallow, ShallowNarrow, XWide };
 // QKV Linear and GLU, 0.5% and 1.9% of a diffusion transformer). 64-deep k-steps when k
 // allows. GLU pairs whole 32-column groups per wavefront, so it takes 64 or 192. A
 // 128-column tile with 64-deep steps never wins this cost: a 128-column grid needs at
-// least half the rounds of the 64-column one, so it is not built.
+// least half the rounds of the 64-column one, so it is not built. A single 64-deep k-step
+// over more than four rounds of tiles (the 64-channel pair widths' Linears over N^2 rows)
+// runs three workgroups per CU with a 2-slot ring: each tile is one load, one step and its
+// store, so more tiles in flight hide more of that latency (template block at N=768: its
+// Linears 1309 -> 1221 us).
 RingPick pick_ring(const GemmArgs &p, int64_t batch, bool glu, int cus) {
   const int64_t mt = ceil_div(p.M, 128) * batch, slots = 2 * int64_t(cus);
   auto rounds = [&](int bn) { return ceil_div(mt * ceil_div(p.N, bn), slots); };
+  if (p.K == 64 && rounds(64) > 4) return RingPick::Skinny;
   if (p.K % 64 != 0) return (p.N <= 64 || rounds(64) <= 1) ? RingPick::ShallowNarrow : RingPick::Shallow;
   if (p.N <= 64 || rounds(64) <= 1) return RingPick::Narrow;
   RingPick best = RingPick::Narrow;
@@ -522,15 +528,17 @@ int gemm_ring(const GemmArgs &p, int64_t batch, int out_dtype, bool glu, hipStre
   q.xcd_split = (!glu && p.K % 64 == 0 && int64_t(p.N) * p.K * 2 <= (int64_t(5) << 19) && p.N > bn &&
                  ceil_div(p.M, 128) * ceil_div(p.N, bn) >= cus) ? 1 : 0;
   // The configuration is observable through the kernel timer of that name.
-  static const char *const names[5][2] = {{"gemm_ring.mid", "gemm_ring.mid+xcd"},
+  static const char *const names[6][2] = {{"gemm_ring.mid", "gemm_ring.mid+xcd"},
                                           {"gemm_ring.narrow", "gemm_ring.narrow+xcd"},
                                           {"gemm_ring.shallow", "gemm_ring.shallow+xcd"},
                                           {"gemm_ring.shallow_narrow", "gemm_ring.shallow_narrow+xcd"},
-                                          {"gemm_ring.xwide", "gemm_ring.xwide+xcd"}};
+                                          {"gemm_ring.xwide", "gemm_ring.xwide+xcd"},
+                                          {"gemm_ring.skinny", "gemm_ring.skinny+xcd"}};
   KernelTimer config_timer(names[int(pick)][q.xcd_split ? 1 : 0], s);
   switch (pick) {
     case RingPick::Mid: return launch_ring<RingMid>(q, batch, out_dtype, glu, s, timer);
     case RingPick::XWide: return launch_ring<RingXWide>(q, batch, out_dtype, glu, s, timer);
+    case RingPick::Skinny: return launch_ring<RingSkinny>(q, batch, out_dtype, glu, s, timer);
     case RingPick::Narrow: return launch_ring<RingNarrow>(q, batch, out_dtype, glu, s, timer);
     case RingPick::Shallow: return launch_ring<RingShallow>(q, batch, out_dtype, glu, s, timer);
     default: return launch_ring<RingShallowNarrow>(q, batch, out_dtype, glu, s, timer);
