@@ -648,10 +648,38 @@ int xfh_grid_self_attention(const void *pair, int pair_dtype, const void *mask, 
   a.bias = p.bias; a.bias_dtype = dtype;
   a.bs[0] = 0; a.bs[1] = 1; a.bs[2] = n * heads; a.bs[3] = heads;
   a.scale = 1.0f / std::sqrt(float(dh));
-  // bf16: the pipelined attention kernel on operands repacked from the projections (the
-  // per-query kernel of attention.hip keeps fp32 and the shapes it does not take).
-  if (p.mha_ws && mha_supported(a, dtype)) XFH_TRY(mha(a, p.mha_ws, p.mha_bytes, s));
-  else XFH_TRY(attention(a, dtype, s));
+  // bf16: the pipelined attention kernel on operands repacked from the projections: whole
+  // projection rows through LDS (qkv_repack) where the width allows, else mha_prepare's
+  // strided reads; the per-query kernel of attention.hip keeps fp32 and the shapes neither takes.
+  bool done = false;
+  if (p.mha_ws && dtype == XFH_BF16) {
+    const int64_t npad = align_up(n, 64), dp = dh <= 16 ? 16 : dh <= 32 ? 32 : 64;
+    Carver mc(p.mha_ws, p.mha_bytes);
+    bf16 *oq = static_cast<bf16 *>(mc.take(n * heads * n * dp * 2));
+    bf16 *ok = static_cast<bf16 *>(mc.take(n * heads * npad * dp * 2));
+    bf16 *ovt = static_cast<bf16 *>(mc.take(n * heads * dp * npad * 2));
+    float *obias = static_cast<float *>(mc.take(heads * n * npad * 4));
+    uint64_t *owords = static_cast<uint64_t *>(mc.take(n * (npad / 64) * 8));
+    if (mc.used <= p.mha_bytes &&
+        qkv_repack(static_cast<const bf16 *>(p.qkv), qkv_ld, n, n, heads, dh, transpose, kLog2e * a.scale, oq, ok,
+                   ovt, s) == XFH_OK) {
+      const int64_t shape[4] = {1, heads, n, n}, strides[4] = {0, 1, n * heads, heads};
+      XFH_TRY(attention_bias_pack(p.bias, dtype, shape, strides, obias, s));
+      XFH_TRY(attention_mask_words(mask, mask_dtype, n, n, n, owords, s));
+      GridAttentionArgs ga;
+      ga.q = oq; ga.k = ok; ga.vt = ovt; ga.bias = obias; ga.maskbits = owords;
+      ga.out = static_cast<bf16 *>(p.attn);
+      ga.osb = row_b * c; ga.ost = row_t * c; ga.ohs = dh;
+      ga.B = int(n); ga.H = int(heads); ga.Nq = int(n); ga.N = int(n);
+      ga.Npad = int(npad); ga.Nblk = int(npad / 64); ga.mbs = ga.Nblk; ga.Dv = int(dh);
+      XFH_TRY(mha_attention(ga, int(dp), s));
+      done = true;
+    }
+  }
+  if (!done) {
+    if (p.mha_ws && mha_supported(a, dtype)) XFH_TRY(mha(a, p.mha_ws, p.mha_bytes, s));
+    else XFH_TRY(attention(a, dtype, s));
+  }
   // attn <- sigmoid(LN(z) Wgate^T) * attn, in place.
   g = gemm_args(p.normed, c, gating_w, c, p.attn, c, plane, c, c);
   g.epi = XFH_EPI_SIGMOID_MUL_AUX; g.aux = p.attn; g.ldaux = c;

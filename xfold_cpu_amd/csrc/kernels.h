@@ -160,6 +160,10 @@ int grid_output(const GridOutputArgs &a, int pair_dtype, int out_dtype, hipStrea
 int64_t grid_attention_pad(int64_t n);
 // The same kernel for head dims 32 and 64 (d = 32 or 64) at the shapes of dot_product_attention.
 int mha_attention(const GridAttentionArgs &a, int d, hipStream_t s);
+// The grid attention's operands at head dim padded_dim(dh) from row-major [q | k | v]
+// projection rows of stride ld (B = T batch rows, pair order; transpose: the ending node).
+int qkv_repack(const bf16 *qkv, int64_t ld, int64_t B, int64_t T, int64_t H, int64_t dh, int transpose, float scale,
+               bf16 *q, bf16 *k, bf16 *vt, hipStream_t s);
 int64_t grid_attention_max_n();
 int grid_attention(const GridAttentionArgs &a, hipStream_t s);
 

@@ -365,4 +365,79 @@ int attention_bias_pack(const void *bias, int dtype, const int64_t *shape, const
   return check_launch("attention_bias_pack");
 }
 
+namespace {
+
+// Operands of the grid attention at widths off the fast path, from the row-major projection
+// rows [q | k | v] (row stride ld, c = H dh columns each): workgroup = (batch row b, 64
+// tokens). The tile's rows are read whole (16-byte pieces) into LDS; q (times scale), k and
+// v^T (the kernel's key order) are written as runs of the kernel's layouts at head dim D,
+// zero beyond dh and for tokens >= T. Row (b, t) of the projection is pair row b n + t, or
+// t n + b for the ending node (transpose).
+constexpr int kRepackTokens = 64;
+__global__ __launch_bounds__(256) void qkv_repack_kernel(const bf16 *__restrict__ qkv, int64_t ld, int T, int Tpad,
+                                                         int H, int dh, int D, int transpose, float scale,
+                                                         bf16 *__restrict__ q, bf16 *__restrict__ k,
+                                                         bf16 *__restrict__ vt) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int c = H * dh, width = 3 * c, lw = width + 8;        // LDS row: 16 bytes of padding
+  bf16 *tile = reinterpret_cast<bf16 *>(smem);
+  const int b = blockIdx.y, t0 = blockIdx.x * kRepackTokens, tid = threadIdx.x;
+  const int chunks = width / 8;
+  for (int i = tid; i < kRepackTokens * chunks; i += 256) {
+    const int t = i / chunks, ch = i - t * chunks, tok = t0 + t;
+    bf16x8 v = {};
+    if (tok < T) {
+      const int64_t row = transpose ? int64_t(tok) * T + b : int64_t(b) * T + tok;
+      v = *reinterpret_cast<const bf16x8 *>(qkv + row * ld + ch * 8);
+    }
+    *reinterpret_cast<bf16x8 *>(tile + t * lw + ch * 8) = v;
+  }
+  __syncthreads();
+  const int dc = D / 8;
+  // q and k: thread = (head, token, 8-dim chunk)
+  for (int i = tid; i < H * kRepackTokens * dc; i += 256) {
+    const int ch = i % dc, rest = i / dc, t = rest % kRepackTokens, h = rest / kRepackTokens, tok = t0 + t;
+    bf16x8 vq, vk;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int d = ch * 8 + e;
+      const bool in = d < dh && tok < T;
+      vq[e] = bf16(in ? static_cast<float>(tile[t * lw + h * dh + d]) * scale : 0.f);
+      vk[e] = in ? tile[t * lw + c + h * dh + d] : bf16(0.f);
+    }
+    const int64_t bh = int64_t(b) * H + h;
+    if (tok < T) *reinterpret_cast<bf16x8 *>(q + (bh * T + tok) * D + ch * 8) = vq;
+    *reinterpret_cast<bf16x8 *>(k + (bh * Tpad + tok) * D + ch * 8) = vk;
+  }
+  // v^T: thread = (head, dim, 8-position group); position p of a run of 32 holds key
+  // 4g + j (p = 8g + j, j < 4) or 16 + 4g + j - 4 (j >= 4).
+  for (int i = tid; i < H * D * (kRepackTokens / 8); i += 256) {
+    const int g8 = i % (kRepackTokens / 8), rest = i / (kRepackTokens / 8), d = rest % D, h = rest / D;
+    bf16x8 v;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int pos = g8 * 8 + e, run = pos & ~31, w = pos & 31, g = w >> 3, j = w & 7;
+      const int key = run + (j < 4 ? 4 * g + j : 16 + 4 * g + j - 4);
+      v[e] = (d < dh && t0 + key < T) ? tile[key * lw + 2 * c + h * dh + d] : bf16(0.f);
+    }
+    *reinterpret_cast<bf16x8 *>(vt + ((int64_t(b) * H + h) * D + d) * Tpad + t0 + g8 * 8) = v;
+  }
+}
+
+}  // namespace
+
+int qkv_repack(const bf16 *qkv, int64_t ld, int64_t B, int64_t T, int64_t H, int64_t dh, int transpose, float scale,
+               bf16 *q, bf16 *k, bf16 *vt, hipStream_t s) {
+  const int D = padded_dim(dh);
+  const int64_t c = H * dh, tpad = align_up(T, 64), lds = kRepackTokens * (3 * c + 8) * 2;
+  if (D == 0 || c % 8 || ld % 8 || ld < 3 * c || lds > 65536 || B > 65535 || tpad > grid_attention_max_n() ||
+      reinterpret_cast<uintptr_t>(qkv) % 16)
+    return fail(XFH_EUNSUPPORTED, "qkv_repack: unsupported shape");
+  if (B * T == 0) return XFH_OK;
+  const dim3 grid(unsigned(tpad / kRepackTokens), unsigned(B));
+  qkv_repack_kernel<<<grid, 256, size_t(lds), s>>>(qkv, ld, int(T), int(tpad), int(H), int(dh), D, transpose, scale,
+                                                   q, k, vt);
+  return check_launch("qkv_repack");
+}
+
 }  // namespace xfh
