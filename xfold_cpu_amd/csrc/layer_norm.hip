@@ -7,6 +7,8 @@
 // butterfly steps inside the wavefront. Statistics are fp32 and two-pass (mean, then
 // the mean of squared deviations) from registers, matching F.layer_norm's biased
 // variance (xfold/fastnn/layer_norm.py:56-59).
+#include <type_traits>
+
 #include "common.h"
 
 namespace xfh {
@@ -185,12 +187,34 @@ __global__ __launch_bounds__(256) void ln_planes_tiled(const TI *__restrict__ x,
   const int64_t r0 = int64_t(blockIdx.x) * kPlaneRows;
   const int l = threadIdx.x & 63, grp = threadIdx.x >> 6;
   const int rows = int(plane - r0 < kPlaneRows ? plane - r0 : kPlaneRows);
-  float s = 0.f;
-  for (int c = grp; c < C; c += 4) {
-    const float v = l < rows ? to_f32(x[int64_t(c) * plane + r0 + l]) : 0.f;
-    tile[c * P + l] = v;
-    s += v;
+  if (plane % 4 == 0) {
+    // 4 rows of one plane per load (8 or 16 bytes; plane % 4 == 0 keeps them aligned)
+    for (int i = threadIdx.x; i < C * (kPlaneRows / 4); i += 256) {
+      const int c = i / (kPlaneRows / 4), l4 = (i - c * (kPlaneRows / 4)) * 4;
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      const TI *src = x + int64_t(c) * plane + r0 + l4;
+      if (l4 + 4 <= rows) {
+        if constexpr (std::is_same<TI, float>::value) {
+          const float4 u = *reinterpret_cast<const float4 *>(src);
+          v[0] = u.x; v[1] = u.y; v[2] = u.z; v[3] = u.w;
+        } else {
+          const bf16x4 u = *reinterpret_cast<const bf16x4 *>(src);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = static_cast<float>(u[e]);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = l4 + e < rows ? to_f32(src[e]) : 0.f;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile[c * P + l4 + e] = v[e];
+    }
+  } else {
+    for (int c = grp; c < C; c += 4) tile[c * P + l] = l < rows ? to_f32(x[int64_t(c) * plane + r0 + l]) : 0.f;
   }
+  __syncthreads();
+  float s = 0.f;
+  for (int c = grp; c < C; c += 4) s += tile[c * P + l];
   part[grp][l] = s;
   __syncthreads();
   if (grp == 0) mean_s[l] = (part[0][l] + part[1][l] + part[2][l] + part[3][l]) / float(C);
@@ -205,6 +229,29 @@ __global__ __launch_bounds__(256) void ln_planes_tiled(const TI *__restrict__ x,
   __syncthreads();
   if (grp == 0) rstd_s[l] = rsqrtf((part[0][l] + part[1][l] + part[2][l] + part[3][l]) / float(C) + eps);
   __syncthreads();
+  if (C % 4 == 0) {                                 // 4 channels of one row per store
+    const int c4s = C / 4;
+    for (int i = threadIdx.x; i < rows * c4s; i += 256) {
+      const int row = i / c4s, c = (i - row * c4s) * 4;
+      float t[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t[e] = (tile[(c + e) * P + row] - mean_s[row]) * rstd_s[row];
+        if (w) t[e] *= w[c + e];
+        if (b) t[e] += b[c + e];
+      }
+      TO *dst = y + (r0 + row) * int64_t(C) + c;
+      if constexpr (std::is_same<TO, float>::value) {
+        *reinterpret_cast<float4 *>(dst) = make_float4(t[0], t[1], t[2], t[3]);
+      } else {
+        bf16x4 u;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) u[e] = bf16(t[e]);
+        *reinterpret_cast<bf16x4 *>(dst) = u;
+      }
+    }
+    return;
+  }
   const int total = rows * C;
   for (int i = threadIdx.x; i < total; i += 256) {
     const int row = i / C, c = i - row * C;
