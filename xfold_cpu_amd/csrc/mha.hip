@@ -431,7 +431,7 @@ int qkv_repack(const bf16 *qkv, int64_t ld, int64_t B, int64_t T, int64_t H, int
   const int D = padded_dim(dh);
   const int64_t c = H * dh, tpad = align_up(T, 64), lds = kRepackTokens * (3 * c + 8) * 2;
   if (D == 0 || c % 8 || ld % 8 || ld < 3 * c || lds > 65536 || B > 65535 || tpad > grid_attention_max_n() ||
-      reinterpret_cast<uintptr_t>(qkv) % 16)
+      reinterpret_cast<uintptr_t>(qkv) % 16 || (transpose && B != T))
     return fail(XFH_EUNSUPPORTED, "qkv_repack: unsupported shape");
   if (B * T == 0) return XFH_OK;
   const dim3 grid(unsigned(tpad / kRepackTokens), unsigned(B));
